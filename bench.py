@@ -1,0 +1,311 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X matmul hot path (BASELINE.json metric).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+
+Workload (the metric's headline): int8-weight GEMV,
+m = 1, A[1, 4096] fp32 ~ N(0, 1) times W[4096, 4096] ~ N(0, 0.02) quantised
+by this library's quantize_q8 (bit-exact with quant.cpp). POOL copies of
+(W_q, scale) -- over 512 MiB -- are visited in turn so each product reads its
+weights from HBM, not from the 256 MB Infinity Cache. One step is one sweep
+over the pool (POOL products, each on its own weights). The timed region
+replays a HIP graph of one step K times: products are launched back to back
+as a decode loop would launch them (the reference also replays its decode
+step as a graph, cuda_model.cu:189-230), so the host's launch cost does not
+hide the kernel.
+
+value = algorithmic bytes (W + scales + A + C) x products / seconds, in GB/s.
+The JSON line also carries:
+  roofline     the GEMV kernel's bytes per launch / its average launch time
+               from HIP events over the timed region, against 8 TB/s HBM
+  cpu_baseline the reference's own matmul_parallel (oracle/_ref, built from
+               /root/reference/src with amdclang++ -O3) on the box's host
+               cores, same inputs, median as bench_matmul.cpp:49-63
+  extra        the metric's second half (fp32 GEMM N = 4096 on MFMA, TFLOPS
+               and % of the 157.3 TFLOPS fp32 MFMA peak), int8 GEMV at
+               m = 4/16/64, fp32 GEMV m = 1, and the reference's own timing
+               convention (host launch -> synchronize, median)
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
+FP32_MFMA_PEAK_TFLOPS = 157.3
+METRIC = "int8 GEMV HBM GB/s (m=1, 4096²) + fp32 GEMM TFLOPS (N=4096), % of peak"
+DIM = 4096
+POOL_MIN_BYTES = 600 << 20   # > 512 MiB
+
+
+def load_engine():
+    spec = importlib.util.spec_from_file_location(
+        "llm_engine_amd", os.path.join(ROOT, "llm-engine_amd", "__init__.py"))
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["llm_engine_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def gemv_bytes(m: int, k: int, n: int, q8: bool) -> int:
+    """Algorithmic bytes: W + (int8) scales + A + C."""
+    return k * n * (1 if q8 else 4) + (4 * n if q8 else 0) + 4 * m * k + 4 * m * n
+
+
+class Pool:
+    """POOL copies of a K x N weight matrix (int8 + scales, or fp32) on the GPU."""
+
+    def __init__(self, em, torch, q8: bool, k: int, n: int, copies: int, seed: int):
+        self.q8 = q8
+        self.ws, self.scales = [], []
+        g = torch.Generator(device="cuda")
+        for i in range(copies):
+            g.manual_seed(seed + i)
+            W = torch.randn((k, n), generator=g, device="cuda", dtype=torch.float32) * 0.02
+            if q8:
+                q, s = em.quantize_q8(W)
+                self.ws.append(q)
+                self.scales.append(s)
+                del W
+            else:
+                self.ws.append(W)
+                self.scales.append(None)
+        torch.cuda.synchronize()
+
+
+def capture_step(em, torch, A, C, pool: Pool):
+    """A HIP graph of one sweep over the pool."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):  # warm the library's scratch outside capture
+        for w, s in zip(pool.ws, pool.scales):
+            em.matmul(A, w, C, scale=s)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for w, s in zip(pool.ws, pool.scales):
+            em.matmul(A, w, C, scale=s)
+    torch.cuda.synchronize()
+    return graph
+
+
+def time_graph(torch, graph, steps: int, warmup: int):
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return start.elapsed_time(end) / 1e3, wall
+
+
+def gemv_case(em, torch, m, q8, steps, warmup, copies=None, seed=1000):
+    k = n = DIM
+    per_copy = k * n * (1 if q8 else 4)
+    copies = copies or max(2, -(-POOL_MIN_BYTES // per_copy))
+    pool = Pool(em, torch, q8, k, n, copies, seed)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7 + m)
+    A = torch.randn((m, k), generator=g, device="cuda", dtype=torch.float32)
+    C = torch.empty((m, n), device="cuda", dtype=torch.float32)
+    graph = capture_step(em, torch, A, C, pool)
+    secs, wall = time_graph(torch, graph, steps, warmup)
+    calls = steps * copies
+    nbytes = gemv_bytes(m, k, n, q8)
+    out = {"m": m, "q8": q8, "copies": copies, "pool_MiB": round(copies * per_copy / 2**20, 1),
+           "calls": calls, "us_per_call": secs / calls * 1e6,
+           "GBps": nbytes * calls / secs / 1e9, "bytes_per_call": nbytes,
+           "wall_s": wall, "secs": secs, "flops_per_call": 2 * m * k * n}
+    del graph, pool
+    torch.cuda.synchronize()
+    return out, (A, C)
+
+
+def host_median_convention(em, torch, A, w, s, C, reps=101):
+    """The reference's bench_cuda convention: host time launch -> synchronize."""
+    em.matmul(A, w, C, scale=s)
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        em.matmul(A, w, C, scale=s)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+def gemm_case(em, torch, N=4096, reps=20):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(3)
+    A = torch.rand((N, N), generator=g, device="cuda") * 2 - 1
+    B = torch.rand((N, N), generator=g, device="cuda") * 2 - 1
+    C = torch.empty((N, N), device="cuda")
+    for _ in range(3):
+        em.matmul(A, B, C, kernel="tiled")
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        em.matmul(A, B, C, kernel="tiled")
+    end.record()
+    torch.cuda.synchronize()
+    secs = start.elapsed_time(end) / 1e3 / reps
+    tflops = 2 * N**3 / secs / 1e12
+    return {"N": N, "ms": secs * 1e3, "TFLOPS": tflops,
+            "pct_of_fp32_mfma_peak": 100 * tflops / FP32_MFMA_PEAK_TFLOPS}, (A, B)
+
+
+def cpu_threads() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def cpu_baseline(A_dev, q_dev, s_dev, gemm_AB):
+    """The reference's matmul_parallel (oracle/_ref) on the host, same inputs."""
+    import numpy as np
+    import oracle
+    ref = oracle.ref()
+    if ref is None:
+        return None
+    threads = cpu_threads()
+    A = A_dev.cpu().numpy()
+    q = q_dev.cpu().numpy()
+    s = s_dev.cpu().numpy()
+    # Bounded sample: one warm-up, then the median of up to 2001 reps (a few s).
+    one = ref.time_parallel_q8(A, q, s, 1, threads)
+    reps = int(max(15, min(2001, 3.0 / max(one, 1e-6)))) | 1
+    secs = ref.time_parallel_q8(A, q, s, reps, threads)
+    nbytes = gemv_bytes(A.shape[0], q.shape[0], q.shape[1], True)
+    out = {"value": nbytes / secs / 1e9, "unit": "GB/s", "cores": threads, "kind": "reference",
+           "sample": f"int8 GEMV m=1 4096x4096 (one W, no rotation), matmul_parallel, "
+                     f"median of {reps} reps after 1 warm-up",
+           "ms": secs * 1e3, "compiler": ref.compiler().split("(")[0].strip(),
+           "library": os.path.basename(ref.path), "pool_threads": ref.pool_size()}
+    if gemm_AB is not None:
+        Ah = gemm_AB[0].cpu().numpy()
+        Bh = gemm_AB[1].cpu().numpy()
+        gs = ref.time_parallel_f32(Ah, Bh, 3, threads)
+        out["gemm_fp32_N4096"] = {"ms": gs * 1e3, "GFLOPS": 2 * 4096**3 / gs / 1e9,
+                                  "sample": "median of 3 reps (reps_for(4096), bench_matmul.cpp:43-48)"}
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[1])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one MI355X: every box in this run has one GPU, and the matmul "
+              "path has no multi-GPU code (it would shard W by output columns, one slab per GPU; "
+              "see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+    em = load_engine()
+    if not torch.cuda.is_available() or not em.available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+
+    head, (A1, _) = gemv_case(em, torch, 1, True, args.steps, args.warmup)
+    steps = args.steps
+    secs = head["secs"]
+    avg_launch_s = secs / head["calls"]
+    achieved = head["bytes_per_call"] / avg_launch_s / 1e9
+    result = {
+        "metric": METRIC,
+        "value": round(head["GBps"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": secs / steps * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 weights, fp32 activations and accumulation",
+        "data": "synthetic: A ~ N(0,1), W ~ N(0,0.02) quantised on the GPU (bit-exact quant.cpp)",
+        "config": {"workload": "int8 GEMV m=1, A[1,4096] x Wq[4096,4096] + fp32 scales "
+                               "(BASELINE configs[1]); one step = one sweep over "
+                               f"{head['copies']} weight copies ({head['pool_MiB']} MiB), "
+                               "HIP-graph replay",
+                   "m": 1, "k": DIM, "n": DIM, "weight_pool_copies": head["copies"],
+                   "pct_of_hbm_peak": round(100 * head["GBps"] / HBM_PEAK_GBS, 2)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "gemv_kernel<int8,1,16,8>",
+                     "avg_launch_us": round(avg_launch_s * 1e6, 3),
+                     "bytes_per_launch": head["bytes_per_call"]},
+    }
+
+    extra = {}
+    q_keep = None
+    gemm_AB = None
+    if not args.no_extra:
+        for m in (4, 16, 64):
+            r, _ = gemv_case(em, torch, m, True, max(5, steps // 2), 2)
+            t_mfma = r["flops_per_call"] / (FP32_MFMA_PEAK_TFLOPS * 1e12)
+            t_hbm = r["bytes_per_call"] / (HBM_PEAK_GBS * 1e9)
+            extra[f"int8_gemv_m{m}"] = {"us": round(r["us_per_call"], 3),
+                                        "GBps": round(r["GBps"], 1),
+                                        "TFLOPS": round(r["flops_per_call"] / r["us_per_call"] / 1e6, 2),
+                                        "bound": "mfma" if t_mfma > t_hbm else "hbm",
+                                        "pct_of_roofline": round(100 * max(t_mfma, t_hbm) * 1e6 / r["us_per_call"], 1)}
+        r, _ = gemv_case(em, torch, 1, False, max(5, steps // 2), 2)
+        extra["fp32_gemv_m1"] = {"us": round(r["us_per_call"], 3), "GBps": round(r["GBps"], 1),
+                                 "pct_of_hbm_peak": round(100 * r["GBps"] / HBM_PEAK_GBS, 1)}
+        gemm, gemm_AB = gemm_case(em, torch)
+        extra["fp32_gemm_N4096"] = {k: round(v, 3) if isinstance(v, float) else v
+                                    for k, v in gemm.items()}
+        # The reference's own convention (bench_cuda.cpp:41-54): host time of
+        # one launch -> synchronize, median of 101, one W (cache-resident).
+        pool = Pool(em, torch, True, DIM, DIM, 1, 99)
+        C = torch.empty((1, DIM), device="cuda")
+        host_s = host_median_convention(em, torch, A1, pool.ws[0], pool.scales[0], C)
+        extra["reference_convention_int8_m1"] = {
+            "ms": round(host_s * 1e3, 4),
+            "GBps_of_B": round(DIM * DIM / host_s / 1e9, 1),
+            "note": "host launch->sync median, single W (cache-resident), as bench_cuda.cpp"}
+        q_keep = (pool.ws[0], pool.scales[0])
+        result["extra"] = extra
+        result["config"]["fp32_gemm_N4096_TFLOPS"] = extra["fp32_gemm_N4096"]["TFLOPS"]
+        result["config"]["fp32_gemm_pct_of_mfma_peak"] = \
+            extra["fp32_gemm_N4096"]["pct_of_fp32_mfma_peak"]
+
+    if not args.no_cpu:
+        if q_keep is None:
+            pool = Pool(em, torch, True, DIM, DIM, 1, 99)
+            q_keep = (pool.ws[0], pool.scales[0])
+        cb = cpu_baseline(A1, q_keep[0], q_keep[1], gemm_AB)
+        if cb is not None:
+            result["cpu_baseline"] = cb
+
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

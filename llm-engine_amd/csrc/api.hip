@@ -1,0 +1,290 @@
+// The C ABI (include/llm_engine_amd.h): argument checks, kernel choice and
+// the library-owned scratch. Replaces the host half of
+// /root/reference/src/cuda_matmul.cu (matmul_impl :399-448, Scratch
+// :268-297, DeviceTensor/DeviceQTensor memory :452-525, entry points
+// :527-574).
+//
+// Every argument is checked on the host before any HIP call, so each error
+// path can be exercised without a GPU. Errors come back as status codes with
+// a message for em_last_error(); the messages name both shapes as
+// "(A is MxK, B is KxN)", as the reference's exceptions do.
+#include <atomic>
+#include <cstdlib>
+#include <mutex>
+#include <string>
+#include <type_traits>
+
+#include "internal.hpp"
+#include "llm_engine_amd.h"
+
+namespace em {
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& msg) {
+    g_error = msg;
+    return code;
+}
+
+std::mutex g_scratch_mu;
+float* g_scratch[kSlots] = {};
+std::size_t g_scratch_cap[kSlots] = {};
+std::atomic<std::size_t> g_generation{0};
+
+bool device_present() {
+    int count = 0;
+    return hipGetDeviceCount(&count) == hipSuccess && count > 0;
+}
+
+// a * b >= 2^31, without overflow: the kernels index with int
+// (cuda_matmul.cu:414-417).
+bool too_many(std::size_t a, std::size_t b) {
+    constexpr std::size_t kLimit = (std::size_t{1} << 31) - 1;
+    return a != 0 && b > kLimit / a;
+}
+
+std::string shapes(std::size_t m, std::size_t n, std::size_t k) {
+    return "(A is " + std::to_string(m) + "x" + std::to_string(k) + ", B is " + std::to_string(k) +
+           "x" + std::to_string(n) + ")";
+}
+
+template <class BT>
+int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, const BT* B,
+                 const float* scale, float* C, int kernel, int accumulate,
+                 const float* rms_weight, void* stream) {
+    if (kernel < EM_KERNEL_AUTOMATIC || kernel > EM_KERNEL_SKINNY)
+        return fail(EM_EINVAL, "matmul_cuda: unknown kernel " + std::to_string(kernel));
+    if (kernel == EM_KERNEL_AUTOMATIC)
+        kernel = m <= 8 ? EM_KERNEL_SKINNY : m <= 64 ? EM_KERNEL_TILED_SPLIT : EM_KERNEL_TILED;
+    if (kernel == EM_KERNEL_SKINNY && m > 8)
+        return fail(EM_EINVAL,
+                    "matmul_cuda: skinny kernel takes at most 8 rows " + shapes(m, n, k));
+    if (too_many(m, k) || too_many(k, n) || too_many(m, n))
+        return fail(EM_EINVAL, "matmul_cuda: more than 2^31 elements " + shapes(m, n, k));
+    if (m == 0 || n == 0) return EM_OK;
+    if (!C) return fail(EM_EINVAL, "matmul_cuda: C is null " + shapes(m, n, k));
+    if (k && (!A || !B))
+        return fail(EM_EINVAL, "matmul_cuda: A or B is null " + shapes(m, n, k));
+    if (std::is_same<BT, int8_t>::value && k && !scale)
+        return fail(EM_EINVAL, "matmul_cuda: int8 B needs its column scales " + shapes(m, n, k));
+    if (!device_present()) return fail(EM_ENODEV, "matmul_cuda: no usable GPU");
+
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    try {
+        if (k == 0) {
+            if (!accumulate) run_fill_zero(C, m * n, s);
+            hip_check(hipGetLastError(), "launch");
+            return EM_OK;
+        }
+        MatmulArgs a{};
+        a.m = static_cast<int>(m);
+        a.n = static_cast<int>(n);
+        a.k = static_cast<int>(k);
+        a.A = A;
+        a.B = B;
+        a.scale = scale;
+        a.C = C;
+        a.accumulate = accumulate != 0;
+        a.rms_weight = rms_weight;
+        a.stream = s;
+        if (rms_weight && kernel != EM_KERNEL_SKINNY) {
+            float* normed = scratch(kNorm, m * k);
+            run_rmsnorm_rows(a.m, a.k, A, rms_weight, normed, s);
+            a.A = normed;
+            a.rms_weight = nullptr;
+        }
+        switch (kernel) {
+            case EM_KERNEL_NAIVE: run_naive<BT>(a); break;
+            case EM_KERNEL_TILED: run_tiled<BT>(a); break;
+            case EM_KERNEL_TILED_SPLIT:
+                if (tiled_split_supports<BT>(a)) {
+                    run_tiled_split<BT>(a);
+                } else {
+                    run_tiled<BT>(a);
+                }
+                break;
+            default: run_skinny<BT>(a); break;
+        }
+        hip_check(hipGetLastError(), "launch");
+    } catch (const DeviceError& e) {
+        return fail(EM_EDEVICE, e.what());
+    } catch (const std::exception& e) {
+        return fail(EM_EDEVICE, std::string("hip: ") + e.what());
+    }
+    return EM_OK;
+}
+
+}  // namespace
+
+float* scratch(ScratchSlot slot, std::size_t floats) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (floats > g_scratch_cap[slot]) {
+        // Queued kernels may still read the old buffer.
+        hip_check(hipDeviceSynchronize(), "synchronize before scratch growth");
+        if (g_scratch[slot]) hip_check(hipFree(g_scratch[slot]), "free scratch");
+        g_scratch[slot] = nullptr;
+        g_scratch_cap[slot] = 0;
+        void* p = nullptr;
+        hip_check(hipMalloc(&p, floats * sizeof(float)), "alloc scratch");
+        g_scratch[slot] = static_cast<float*>(p);
+        g_scratch_cap[slot] = floats;
+        g_generation.fetch_add(1);
+    }
+    return g_scratch[slot];
+}
+
+std::size_t scratch_generation() { return g_generation.load(); }
+
+unsigned* tile_counters(std::size_t count) {
+    static unsigned* buf = nullptr;
+    static std::size_t cap = 0;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (count > cap) {
+        hip_check(hipDeviceSynchronize(), "synchronize before counter growth");
+        if (buf) hip_check(hipFree(buf), "free counters");
+        buf = nullptr;
+        cap = 0;
+        void* p = nullptr;
+        const std::size_t want = count < 4096 ? 4096 : count;
+        hip_check(hipMalloc(&p, want * sizeof(unsigned)), "alloc counters");
+        hip_check(hipMemset(p, 0, want * sizeof(unsigned)), "zero counters");
+        hip_check(hipDeviceSynchronize(), "zero counters");
+        buf = static_cast<unsigned*>(p);
+        cap = want;
+        g_generation.fetch_add(1);
+    }
+    return buf;
+}
+
+bool fused_reduce() {
+    static const bool on = [] {
+        const char* v = std::getenv("EM_FUSED_REDUCE");
+        return !(v && v[0] == '0');
+    }();
+    return on;
+}
+
+int cu_count() {
+    static const int cus = [] {
+        int device = 0, n = 0;
+        if (hipGetDevice(&device) != hipSuccess) return 256;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+            return 256;
+        return n > 0 ? n : 256;
+    }();
+    return cus;
+}
+
+}  // namespace em
+
+using em::fail;
+using em::too_many;
+
+extern "C" {
+
+const char* em_last_error(void) { return em::g_error.c_str(); }
+
+int em_available(void) { return em::device_present() ? 1 : 0; }
+
+int em_synchronize(void) {
+    if (!em::device_present()) return fail(EM_ENODEV, "synchronize: no usable GPU");
+    const hipError_t err = hipDeviceSynchronize();
+    if (err != hipSuccess)
+        return fail(EM_EDEVICE, std::string("hip: synchronize: ") + hipGetErrorString(err));
+    return EM_OK;
+}
+
+size_t em_scratch_generation(void) { return em::scratch_generation(); }
+
+int em_malloc(void** ptr, size_t bytes) {
+    if (!ptr) return fail(EM_EINVAL, "em_malloc: null output pointer");
+    *ptr = nullptr;
+    if (bytes == 0) return EM_OK;
+    if (!em::device_present()) return fail(EM_ENODEV, "alloc: no usable GPU");
+    const hipError_t err = hipMalloc(ptr, bytes);
+    if (err != hipSuccess) {
+        *ptr = nullptr;
+        return fail(EM_EDEVICE, std::string("hip: alloc: ") + hipGetErrorString(err));
+    }
+    return EM_OK;
+}
+
+int em_free(void* ptr) {
+    if (!ptr) return EM_OK;
+    const hipError_t err = hipFree(ptr);
+    if (err != hipSuccess)
+        return fail(EM_EDEVICE, std::string("hip: free: ") + hipGetErrorString(err));
+    return EM_OK;
+}
+
+// Synchronous copies, ordered after the calling thread's default-stream work
+// (the stream the C++ layer queues products on), as cudaMemcpy is in the
+// reference's upload() / download().
+static int copy(void* dst, const void* src, size_t bytes, hipMemcpyKind kind, const char* what) {
+    if (bytes == 0) return EM_OK;
+    if (!dst || !src) return fail(EM_EINVAL, std::string(what) + ": null pointer");
+    if (!em::device_present()) return fail(EM_ENODEV, std::string(what) + ": no usable GPU");
+    hipError_t err = hipMemcpyAsync(dst, src, bytes, kind, hipStreamPerThread);
+    if (err == hipSuccess) err = hipStreamSynchronize(hipStreamPerThread);
+    if (err != hipSuccess)
+        return fail(EM_EDEVICE, std::string("hip: ") + what + ": " + hipGetErrorString(err));
+    return EM_OK;
+}
+
+int em_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+    return copy(dst, src, bytes, hipMemcpyHostToDevice, "upload");
+}
+
+int em_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+    return copy(dst, src, bytes, hipMemcpyDeviceToHost, "download");
+}
+
+int em_matmul_f32(size_t m, size_t n, size_t k, const float* A, const float* B, float* C,
+                  int kernel, int accumulate, const float* rms_weight, void* stream) {
+    return em::matmul_entry<float>(m, n, k, A, B, nullptr, C, kernel, accumulate, rms_weight,
+                                   stream);
+}
+
+int em_matmul_q8(size_t m, size_t n, size_t k, const float* A, const int8_t* B,
+                 const float* scale, float* C, int kernel, int accumulate,
+                 const float* rms_weight, void* stream) {
+    return em::matmul_entry<int8_t>(m, n, k, A, B, scale, C, kernel, accumulate, rms_weight,
+                                    stream);
+}
+
+int em_quantize_q8(size_t rows, size_t cols, const float* B, int8_t* q, float* scale,
+                   void* stream) {
+    if (em::too_many(rows, cols))
+        return fail(EM_EINVAL, "quantize_q8: more than 2^31 elements (B is " +
+                                   std::to_string(rows) + "x" + std::to_string(cols) + ")");
+    if (cols == 0) return EM_OK;
+    if (!scale || (rows && (!B || !q))) return fail(EM_EINVAL, "quantize_q8: null pointer");
+    if (!em::device_present()) return fail(EM_ENODEV, "quantize_q8: no usable GPU");
+    try {
+        em::run_quantize_q8(static_cast<int>(rows), static_cast<int>(cols), B, q, scale,
+                            static_cast<hipStream_t>(stream));
+        em::hip_check(hipGetLastError(), "launch");
+    } catch (const std::exception& e) {
+        return fail(EM_EDEVICE, e.what());
+    }
+    return EM_OK;
+}
+
+int em_dequantize_q8(size_t rows, size_t cols, const int8_t* q, const float* scale, float* out,
+                     void* stream) {
+    if (em::too_many(rows, cols)) return fail(EM_EINVAL, "dequantize: more than 2^31 elements");
+    if (rows == 0 || cols == 0) return EM_OK;
+    if (!q || !scale || !out) return fail(EM_EINVAL, "dequantize: null pointer");
+    if (!em::device_present()) return fail(EM_ENODEV, "dequantize: no usable GPU");
+    try {
+        em::run_dequantize_q8(static_cast<int>(rows), static_cast<int>(cols), q, scale, out,
+                              static_cast<hipStream_t>(stream));
+        em::hip_check(hipGetLastError(), "launch");
+    } catch (const std::exception& e) {
+        return fail(EM_EDEVICE, e.what());
+    }
+    return EM_OK;
+}
+
+}  // extern "C"

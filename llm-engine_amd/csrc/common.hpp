@@ -1,0 +1,68 @@
+// Device helpers shared by the gfx950 kernels: wave64 reductions, vector
+// types and the int8 -> fp32 widening.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace em {
+
+// RMSNorm's eps (ops.h:12 of the reference: rmsnorm(..., eps = 1e-5f)).
+constexpr float kRmsEps = 1e-5f;
+
+// Every kernel here runs 256-thread workgroups: four wave64s, one per SIMD.
+constexpr int kThreads = 256;
+constexpr int kWave = 64;
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// Butterfly sum over the 64 lanes of a wave. The pattern is fixed, so the
+// result does not depend on timing.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+// Sum over a 256-thread workgroup; every thread gets the result. The four
+// wave sums are added in wave order. `part` is 4 floats of LDS; the leading
+// barrier lets a previous call finish reading it.
+__device__ __forceinline__ float block_sum(float v, float* part) {
+    v = wave_sum(v);
+    const int wave = threadIdx.x / kWave;
+    __syncthreads();
+    if ((threadIdx.x % kWave) == 0) part[wave] = v;
+    __syncthreads();
+    return (part[0] + part[1]) + (part[2] + part[3]);
+}
+
+// Four int8 in one 32-bit word, widened to fp32. hipcc turns each into one
+// v_cvt_f32_i32 with an SDWA sign-extended byte select.
+__device__ __forceinline__ void widen4(uint32_t w, float* out) {
+    out[0] = static_cast<float>(static_cast<int8_t>(w));
+    out[1] = static_cast<float>(static_cast<int8_t>(w >> 8));
+    out[2] = static_cast<float>(static_cast<int8_t>(w >> 16));
+    out[3] = static_cast<float>(static_cast<int8_t>(w >> 24));
+}
+
+// Split-K arrival: every workgroup of a tile calls this after writing its
+// partial sums. It returns true (in all threads) only in the workgroup that
+// arrives last, which then sees every other workgroup's partials. The
+// device-scope fences write back and invalidate this XCD's L2 as the memory
+// model requires across XCDs; the counter is a plain vector atomic.
+__device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned arrivals, int* flag) {
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) *flag = atomicAdd(counter, 1u) == arrivals - 1u;
+    __syncthreads();
+    const bool last = *flag != 0;
+    if (last) __threadfence();
+    return last;
+}
+
+__device__ __forceinline__ floatx4 mfma16x16x4(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+}  // namespace em

@@ -1,0 +1,372 @@
+// Decode-shaped products, m <= 8 rows of A against a k x n weight matrix:
+// GpuKernel::skinny (reference: sgemm_skinny + run_skinny,
+// /root/reference/src/cuda_matmul.cu:127-243,365-397).
+//
+// The product is bound by reading B once, so the kernel is laid out for HBM:
+//
+//  * A workgroup (256 threads, four wave64s) owns a 256-column tile of C and
+//    a slice of R = E * L rows of B. Each lane loads E consecutive columns of
+//    a row as one 16-byte vector (E = 16 int8 or 4 fp32; 4-byte and scalar
+//    variants cover widths that are not a multiple of 16 bytes), so the
+//    256 / E lanes of a row group read one contiguous 256-column run of a row
+//    (256 B int8, 1 KB fp32) per instruction.
+//  * The tile has E row groups; lane rows are rg, rg + E, ..., so every
+//    lane issues all L of its loads before it uses any: 16 B x L in flight
+//    per lane, and the whole matrix is in flight across the grid at 4096^2.
+//  * int8 is widened in registers (one SDWA convert per byte) and summed
+//    unscaled; the column scale is applied once to the reduced sum, as the
+//    reference's 4-column path and CPU streaming path do
+//    (cuda_matmul.cu:148-153,234-242; matmul.cpp:273-281).
+//  * The E row groups are added in LDS in a fixed order. k slices across
+//    workgroups go to a partial buffer [slice][m][n] and are added in slice
+//    order by reduce_slices, so repeated calls give the same bits
+//    (tests/test_cuda.cpp:221-275 of the reference).
+//  * With a norm weight, each workgroup computes its rows' RMS scales over
+//    all of k and normalises its slice of A as it stages it in LDS
+//    (cuda_matmul.cu:159-170,197,213).
+#include <cstdlib>
+#include <type_traits>
+
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace em {
+namespace {
+
+// E elements of BT per lane and row, loaded as one vector and widened to fp32.
+template <class BT, int E>
+struct Lane;
+
+template <>
+struct Lane<int8_t, 16> {
+    using V = uint4;
+    static __device__ __forceinline__ V load(const int8_t* p) {
+        return *reinterpret_cast<const uint4*>(p);
+    }
+    static __device__ __forceinline__ V zero() { return make_uint4(0, 0, 0, 0); }
+    static __device__ __forceinline__ void widen(const V& v, float* b) {
+        widen4(v.x, b);
+        widen4(v.y, b + 4);
+        widen4(v.z, b + 8);
+        widen4(v.w, b + 12);
+    }
+};
+
+template <>
+struct Lane<int8_t, 4> {
+    using V = uint32_t;
+    static __device__ __forceinline__ V load(const int8_t* p) {
+        return *reinterpret_cast<const uint32_t*>(p);
+    }
+    static __device__ __forceinline__ V zero() { return 0u; }
+    static __device__ __forceinline__ void widen(const V& v, float* b) { widen4(v, b); }
+};
+
+template <>
+struct Lane<int8_t, 1> {
+    using V = int8_t;
+    static __device__ __forceinline__ V load(const int8_t* p) { return *p; }
+    static __device__ __forceinline__ V zero() { return 0; }
+    static __device__ __forceinline__ void widen(const V& v, float* b) {
+        b[0] = static_cast<float>(v);
+    }
+};
+
+template <>
+struct Lane<float, 4> {
+    using V = float4;
+    static __device__ __forceinline__ V load(const float* p) {
+        return *reinterpret_cast<const float4*>(p);
+    }
+    static __device__ __forceinline__ V zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+    static __device__ __forceinline__ void widen(const V& v, float* b) {
+        b[0] = v.x;
+        b[1] = v.y;
+        b[2] = v.z;
+        b[3] = v.w;
+    }
+};
+
+template <>
+struct Lane<float, 1> {
+    using V = float;
+    static __device__ __forceinline__ V load(const float* p) { return *p; }
+    static __device__ __forceinline__ V zero() { return 0.f; }
+    static __device__ __forceinline__ void widen(const V& v, float* b) { b[0] = v; }
+};
+
+template <class BT>
+struct GemvParams {
+    int m, n, k;
+    const float* A;
+    const float* rms_weight;
+    const BT* B;
+    const float* scale;  // int8 only
+    float* out;          // C when direct, else partials [slice][m][n]
+    float* C;            // final output (the fused reduction writes it)
+    unsigned* counters;  // per column tile; null: reduce_slices adds the slices
+    int accumulate;
+    int direct;
+};
+
+// MM: rows of A the kernel is compiled for (m <= MM; extra rows are zero).
+// E: columns per lane. L: rows per lane. NORM: fused RMSNorm of A.
+template <class BT, int MM, int E, int L, bool NORM>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
+    using LT = Lane<BT, E>;
+    using V = typename LT::V;
+    constexpr int LPR = kThreads / E;  // lanes across one 256-column run
+    constexpr int R = E * L;           // rows of B per workgroup
+    constexpr int AREG = (MM * R + kThreads - 1) / kThreads;
+    constexpr int RS = LPR + 1;  // padded stride of the reduction buffer
+    constexpr bool kQ8 = std::is_same<BT, int8_t>::value;
+
+    __shared__ float a_s[MM * R];
+    __shared__ float red[E * E * RS];
+    __shared__ float part[4];
+    __shared__ float rs_s[MM];
+
+    const int tid = threadIdx.x;
+    const int cg = tid % LPR;
+    const int rg = tid / LPR;
+    const int col = blockIdx.x * kThreads + cg * E;
+    const bool active = col < p.n;
+    const int p0 = blockIdx.y * R;
+
+    // This workgroup's slice of A, raw, into registers: issued before the
+    // weight loads so its wait does not include them.
+    float a_reg[AREG];
+#pragma unroll
+    for (int t = 0; t < AREG; ++t) {
+        const int idx = tid + t * kThreads;
+        const int r = idx / R, pp = p0 + idx % R;
+        a_reg[t] = (idx < MM * R && r < p.m && pp < p.k) ? p.A[r * p.k + pp] : 0.0f;
+    }
+
+    // All L weight vectors of this lane in flight at once.
+    V w[L];
+#pragma unroll
+    for (int i = 0; i < L; ++i) {
+        const int pp = p0 + rg + i * E;
+        w[i] = (active && pp < p.k) ? LT::load(p.B + static_cast<size_t>(pp) * p.n + col)
+                                    : LT::zero();
+    }
+
+    if constexpr (NORM) {
+#pragma unroll
+        for (int r = 0; r < MM; ++r) {
+            float ss = 0.0f;
+            if (r < p.m)
+                for (int j = tid; j < p.k; j += kThreads) {
+                    const float v = p.A[r * p.k + j];
+                    ss = fmaf(v, v, ss);
+                }
+            const float total = block_sum(ss, part);
+            if (tid == 0) rs_s[r] = 1.0f / sqrtf(total / static_cast<float>(p.k) + kRmsEps);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int t = 0; t < AREG; ++t) {
+        const int idx = tid + t * kThreads;
+        if (idx < MM * R) {
+            float v = a_reg[t];
+            if constexpr (NORM) {
+                const int r = idx / R, pp = p0 + idx % R;
+                if (r < p.m && pp < p.k) v = v * rs_s[r] * p.rms_weight[pp];
+            }
+            a_s[idx] = v;
+        }
+    }
+    __syncthreads();
+
+    float acc[MM][E];
+#pragma unroll
+    for (int r = 0; r < MM; ++r)
+#pragma unroll
+        for (int j = 0; j < E; ++j) acc[r][j] = 0.0f;
+
+#pragma unroll
+    for (int i = 0; i < L; ++i) {
+        float b[E];
+        LT::widen(w[i], b);
+        const int pl = rg + i * E;
+#pragma unroll
+        for (int r = 0; r < MM; ++r) {
+            const float a = a_s[r * R + pl];
+#pragma unroll
+            for (int j = 0; j < E; ++j) acc[r][j] = fmaf(a, b[j], acc[r][j]);
+        }
+    }
+
+    // Add the E row groups in order, one row of C at a time. Thread t then
+    // owns local column t of the tile.
+    const int ccg = tid / E, cj = tid % E;
+    const int c = blockIdx.x * kThreads + tid;
+#pragma unroll
+    for (int r = 0; r < MM; ++r) {
+        if (r < p.m) {
+#pragma unroll
+            for (int j = 0; j < E; ++j) red[(rg * E + j) * RS + cg] = acc[r][j];
+            __syncthreads();
+            float total = 0.0f;
+#pragma unroll
+            for (int g = 0; g < E; ++g) total += red[(g * E + cj) * RS + ccg];
+            if (c < p.n) {
+                if (p.direct) {
+                    float v = total;
+                    if constexpr (kQ8) v *= p.scale[c];
+                    float* o = p.out + static_cast<size_t>(r) * p.n + c;
+                    *o = p.accumulate ? *o + v : v;
+                } else {
+                    p.out[(static_cast<size_t>(blockIdx.y) * p.m + r) * p.n + c] = total;
+                }
+            }
+            __syncthreads();
+        }
+    }
+
+    // Fused split-K: the last workgroup of this column tile adds the slices
+    // in slice order (so the bits do not depend on arrival order), applies
+    // the column scale and the residual, and re-arms the counter.
+    if (!p.direct && p.counters) {
+        __shared__ int last;
+        if (arrive_last(&p.counters[blockIdx.x], gridDim.y, &last)) {
+            if (c < p.n) {
+                const float s = kQ8 ? p.scale[c] : 1.0f;
+                for (int r = 0; r < p.m; ++r) {
+                    float total = 0.0f;
+                    for (int sl = 0; sl < static_cast<int>(gridDim.y); ++sl)
+                        total += p.out[(static_cast<size_t>(sl) * p.m + r) * p.n + c];
+                    float* o = p.C + static_cast<size_t>(r) * p.n + c;
+                    const float v = total * s;
+                    *o = p.accumulate ? *o + v : v;
+                }
+            }
+            if (tid == 0) p.counters[blockIdx.x] = 0u;
+        }
+    }
+}
+
+// Deepest rows-per-lane that fits the register file without spilling: with
+// 16 int8 columns per lane, more than one row of A holds 32+ accumulators
+// and 16 loads in flight would pass 256 VGPRs.
+constexpr int max_depth(int E, int MM) { return (E == 16 && MM > 1) ? 8 : 16; }
+
+template <class BT, int MM, int E, int L, bool NORM>
+void launch(const GemvParams<BT>& p, dim3 grid, hipStream_t s) {
+    hipLaunchKernelGGL((gemv_kernel<BT, MM, E, L, NORM>), grid, dim3(kThreads), 0, s, p);
+}
+
+template <class BT, int E, int L, bool NORM>
+void pick_rows(const GemvParams<BT>& p, dim3 grid, hipStream_t s) {
+    if (p.m <= 1) {
+        launch<BT, 1, E, L, NORM>(p, grid, s);
+    } else if (p.m <= 2) {
+        launch<BT, 2, E, (L < max_depth(E, 2) ? L : max_depth(E, 2)), NORM>(p, grid, s);
+    } else if (p.m <= 4) {
+        launch<BT, 4, E, (L < max_depth(E, 4) ? L : max_depth(E, 4)), NORM>(p, grid, s);
+    } else {
+        launch<BT, 8, E, (L < max_depth(E, 8) ? L : max_depth(E, 8)), NORM>(p, grid, s);
+    }
+}
+
+template <class BT, int E, bool NORM>
+void pick_depth(int L, const GemvParams<BT>& p, dim3 grid, hipStream_t s) {
+    if constexpr (E == 1) {
+        pick_rows<BT, 1, 16, NORM>(p, grid, s);
+    } else {
+        switch (L) {
+            case 4: pick_rows<BT, E, 4, NORM>(p, grid, s); break;
+            case 8: pick_rows<BT, E, 8, NORM>(p, grid, s); break;
+            default: pick_rows<BT, E, 16, NORM>(p, grid, s); break;
+        }
+    }
+}
+
+template <class BT, bool NORM>
+void pick_width(int E, int L, const GemvParams<BT>& p, dim3 grid, hipStream_t s) {
+    if constexpr (std::is_same<BT, int8_t>::value) {
+        if (E == 16) return pick_depth<BT, 16, NORM>(L, p, grid, s);
+    }
+    if (E == 4) return pick_depth<BT, 4, NORM>(L, p, grid, s);
+    pick_depth<BT, 1, NORM>(L, p, grid, s);
+}
+
+bool aligned(const void* ptr, size_t bytes) {
+    return reinterpret_cast<uintptr_t>(ptr) % bytes == 0;
+}
+
+// Rows per lane: the deepest of 16 / 8 / 4 that still gives the grid about
+// two workgroups per CU. EM_GEMV_ROWS_PER_LANE overrides it (tuning sweeps).
+// The result is what the launched kernel uses: capped by max_depth as
+// pick_rows caps it.
+int rows_per_lane(int E, int m, int n, int k) {
+    static const int forced = [] {
+        const char* v = std::getenv("EM_GEMV_ROWS_PER_LANE");
+        return v ? std::atoi(v) : 0;
+    }();
+    if (E == 1) return 16;
+    const int mm = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
+    const int cap = max_depth(E, mm);
+    int L = 4;
+    if (forced == 4 || forced == 8 || forced == 16) {
+        L = forced;
+    } else {
+        const long long tiles = ceil_div(n, kThreads);
+        const long long target = 2LL * cu_count();
+        for (int depth : {16, 8}) {
+            if (tiles * ceil_div(k, static_cast<long long>(E) * depth) >= target) {
+                L = depth;
+                break;
+            }
+        }
+    }
+    return L < cap ? L : cap;
+}
+
+}  // namespace
+
+template <class BT>
+void run_skinny(const MatmulArgs& a) {
+    const BT* B = static_cast<const BT*>(a.B);
+    int E = 1;
+    if (std::is_same<BT, int8_t>::value && a.n % 16 == 0 && aligned(B, 16)) {
+        E = 16;
+    } else if (a.n % 4 == 0 && aligned(B, 4 * sizeof(BT))) {
+        E = 4;
+    }
+    const int L = rows_per_lane(E, a.m, a.n, a.k);
+    const int rows_per_block = E * (E == 1 ? 16 : L);
+    const int slices = ceil_div(a.k, rows_per_block);
+    const dim3 grid(ceil_div(a.n, kThreads), slices);
+
+    GemvParams<BT> p{};
+    p.m = a.m;
+    p.n = a.n;
+    p.k = a.k;
+    p.A = a.A;
+    p.rms_weight = a.rms_weight;
+    p.B = B;
+    p.scale = a.scale;
+    p.direct = slices == 1;
+    p.accumulate = a.accumulate;
+    p.C = a.C;
+    p.out = p.direct ? a.C
+                     : scratch(kPartial, static_cast<size_t>(slices) * a.m * a.n);
+    p.counters = (!p.direct && fused_reduce()) ? tile_counters(grid.x) : nullptr;
+    if (a.rms_weight) {
+        pick_width<BT, true>(E, L, p, grid, a.stream);
+    } else {
+        pick_width<BT, false>(E, L, p, grid, a.stream);
+    }
+    if (!p.direct && !p.counters)
+        run_reduce_slices(a.m, a.n, slices, p.out,
+                          std::is_same<BT, int8_t>::value ? a.scale : nullptr, a.C,
+                          a.accumulate, a.stream);
+}
+
+template void run_skinny<float>(const MatmulArgs&);
+template void run_skinny<int8_t>(const MatmulArgs&);
+
+}  // namespace em

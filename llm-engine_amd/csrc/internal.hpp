@@ -1,0 +1,95 @@
+// Host-side interface between the C ABI (api.hip) and the kernel files.
+// Every launcher takes already-validated arguments: shapes below 2^31
+// elements, non-null pointers where the shape needs them, and m, n, k > 0.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace em {
+
+// A HIP runtime failure; api.hip turns it into EM_EDEVICE with this text.
+struct DeviceError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+inline void hip_check(hipError_t err, const char* what) {
+    if (err != hipSuccess)
+        throw DeviceError(std::string("hip: ") + what + ": " + hipGetErrorString(err));
+}
+
+// Library-owned, grow-only device scratch (split-K partials, the normed copy
+// of A, quantiser column maxima). Growing waits for the device, frees the old
+// buffer and bumps scratch_generation(). Slot 0 holds partials, slot 1 the
+// norm buffer, slot 2 quantiser work space.
+enum ScratchSlot { kPartial = 0, kNorm = 1, kQuant = 2, kSlots = 3 };
+float* scratch(ScratchSlot slot, std::size_t floats);
+std::size_t scratch_generation();
+
+// Arrival counters for kernels whose last workgroup per column tile adds the
+// k slices itself. Zeroed when allocated; each such kernel's last workgroup
+// puts its counter back to zero, so they are zero between calls.
+unsigned* tile_counters(std::size_t count);
+
+// True unless EM_FUSED_REDUCE=0: split-K sums are added by the last
+// workgroup of each tile instead of a separate reduce_slices launch.
+bool fused_reduce();
+
+// Compute units of the current device (cached).
+int cu_count();
+
+struct MatmulArgs {
+    int m, n, k;
+    const float* A;
+    const void* B;         // float* or int8_t*
+    const float* scale;    // int8 column scales, null for fp32
+    float* C;
+    bool accumulate;
+    const float* rms_weight;  // null: no norm
+    hipStream_t stream;
+};
+
+// Decode-shaped GEMV, m <= 8 (GpuKernel::skinny). Fuses the norm.
+template <class BT>
+void run_skinny(const MatmulArgs& a);
+
+// MFMA over 16/32/64-row tiles with B streamed once and k split across
+// blocks (GpuKernel::tiled_split). A must already be normed.
+template <class BT>
+void run_tiled_split(const MatmulArgs& a);
+
+// LDS-tiled MFMA GEMM (GpuKernel::tiled). A must already be normed.
+template <class BT>
+void run_tiled(const MatmulArgs& a);
+
+// One thread per element (GpuKernel::naive). A must already be normed.
+template <class BT>
+void run_naive(const MatmulArgs& a);
+
+// True if run_tiled_split can take this shape (vector loads of B rows).
+template <class BT>
+bool tiled_split_supports(const MatmulArgs& a);
+
+// out[m x k] = rmsnorm(A) * w, one workgroup per row.
+void run_rmsnorm_rows(int m, int k, const float* A, const float* w, float* out,
+                      hipStream_t stream);
+
+// C[i] = (accumulate ? C[i] : 0) + scale[i % n] * sum_s partial[s][i], s in order.
+void run_reduce_slices(int m, int n, int slices, const float* partial, const float* scale,
+                       float* C, bool accumulate, hipStream_t stream);
+
+// Zero `count` floats with a kernel (not hipMemsetAsync, so graph capture is safe).
+void run_fill_zero(float* p, std::size_t count, hipStream_t stream);
+
+void run_quantize_q8(int rows, int cols, const float* B, int8_t* q, float* scale,
+                     hipStream_t stream);
+void run_dequantize_q8(int rows, int cols, const int8_t* q, const float* scale, float* out,
+                       hipStream_t stream);
+
+inline int ceil_div(long long x, long long d) { return static_cast<int>((x + d - 1) / d); }
+
+}  // namespace em

@@ -1,0 +1,93 @@
+"""The C ABI without a GPU: it loads, exports every symbol include/*.h
+declares, and rejects bad arguments on the host before any HIP call, with
+the reference's messages (cuda_matmul.cu:406-422, test_cuda.cpp:277-287)."""
+import os
+import re
+
+import pytest
+
+from tests import engine
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+em = engine.load()
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "llm_engine_amd.h")).read()
+    return sorted(set(re.findall(r"\b(em_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = em.lib()
+    names = declared_symbols()
+    assert len(names) >= 12
+    for name in names:
+        assert hasattr(lib, name), name
+    assert sorted(em.EXPORTS) == names
+
+
+def test_exports_match_nm():
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", em.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (em_[a-z0-9_]+)$", out, re.M))
+    assert set(declared_symbols()) <= exported
+
+
+def err(fn):
+    with pytest.raises(em.EngineError) as e:
+        fn()
+    return e.value
+
+
+def test_skinny_rejects_more_than_8_rows():
+    e = err(lambda: em.matmul_f32_raw(9, 2, 2, 16, 16, 16, "skinny"))
+    assert e.code == em.EM_EINVAL
+    assert "at most 8 rows" in str(e) and "9x2" in str(e) and "2x2" in str(e)
+
+
+def test_more_than_2_pow_31_elements():
+    e = err(lambda: em.matmul_f32_raw(1 << 16, 1 << 16, 1, 16, 16, 16))
+    assert e.code == em.EM_EINVAL and "2^31" in str(e)
+    e = err(lambda: em.matmul_q8_raw(2, 3, 1 << 30, 16, 16, 16, 16))
+    assert e.code == em.EM_EINVAL and "2^31" in str(e)
+    # Just below the limit is accepted by the checks (no GPU here: no device).
+    e = err(lambda: em.matmul_f32_raw(1, 1, (1 << 31) - 1, 16, 16, 16, "naive"))
+    assert e.code == em.EM_ENODEV
+
+
+def test_unknown_kernel():
+    e = err(lambda: em.matmul_f32_raw(1, 1, 1, 16, 16, 16, 7))
+    assert e.code == em.EM_EINVAL and "unknown kernel" in str(e)
+
+
+def test_null_pointers():
+    assert err(lambda: em.matmul_f32_raw(2, 3, 4, 16, 16, None)).code == em.EM_EINVAL
+    assert err(lambda: em.matmul_f32_raw(2, 3, 4, None, 16, 16)).code == em.EM_EINVAL
+    e = err(lambda: em.matmul_q8_raw(2, 3, 4, 16, 16, None, 16))
+    assert e.code == em.EM_EINVAL and "scales" in str(e)
+    assert err(lambda: em.quantize_q8_raw(3, 3, None, 16, 16)).code == em.EM_EINVAL
+
+
+def test_empty_products_are_no_ops():
+    # m == 0 or n == 0 return before any check that needs a device
+    # (cuda_matmul.cu:418), even with null pointers.
+    em.matmul_f32_raw(0, 5, 7, None, None, None)
+    em.matmul_q8_raw(3, 0, 7, None, None, None, None)
+    em.quantize_q8_raw(5, 0, None, None, None)
+    em.dequantize_q8_raw(0, 4, None, None, None)
+
+
+def test_no_device_is_reported():
+    if em.available():
+        pytest.skip("a GPU is present")
+    e = err(lambda: em.matmul_f32_raw(1, 1, 1, 16, 16, 16))
+    assert e.code == em.EM_ENODEV
+    assert err(em.synchronize).code == em.EM_ENODEV
+    assert em.scratch_generation() == 0
+
+
+def test_skinny_check_precedes_size_check():
+    # As in matmul_impl: kernel choice, then the skinny row limit, then 2^31.
+    e = err(lambda: em.matmul_f32_raw(9, 1 << 16, 1 << 16, 16, 16, 16, "skinny"))
+    assert "at most 8 rows" in str(e)
