@@ -9,7 +9,6 @@
 // a message for em_last_error(); the messages name both shapes as
 // "(A is MxK, B is KxN)", as the reference's exceptions do.
 #include <atomic>
-#include <cstdlib>
 #include <mutex>
 #include <string>
 #include <type_traits>
@@ -136,34 +135,6 @@ float* scratch(ScratchSlot slot, std::size_t floats) {
 
 std::size_t scratch_generation() { return g_generation.load(); }
 
-unsigned* tile_counters(std::size_t count) {
-    static unsigned* buf = nullptr;
-    static std::size_t cap = 0;
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    if (count > cap) {
-        hip_check(hipDeviceSynchronize(), "synchronize before counter growth");
-        if (buf) hip_check(hipFree(buf), "free counters");
-        buf = nullptr;
-        cap = 0;
-        void* p = nullptr;
-        const std::size_t want = count < 4096 ? 4096 : count;
-        hip_check(hipMalloc(&p, want * sizeof(unsigned)), "alloc counters");
-        hip_check(hipMemset(p, 0, want * sizeof(unsigned)), "zero counters");
-        hip_check(hipDeviceSynchronize(), "zero counters");
-        buf = static_cast<unsigned*>(p);
-        cap = want;
-        g_generation.fetch_add(1);
-    }
-    return buf;
-}
-
-bool fused_reduce() {
-    static const bool on = [] {
-        const char* v = std::getenv("EM_FUSED_REDUCE");
-        return !(v && v[0] == '0');
-    }();
-    return on;
-}
 
 int cu_count() {
     static const int cus = [] {

@@ -49,8 +49,7 @@ __global__ __launch_bounds__(kThreads) void reduce_slices_kernel(int mn, int n, 
                                                                  int accumulate) {
     const int i = blockIdx.x * kThreads + threadIdx.x;
     if (i >= mn) return;
-    float total = 0.0f;
-    for (int s = 0; s < slices; ++s) total += partial[static_cast<size_t>(s) * mn + i];
+    float total = ordered_sum(partial + i, static_cast<size_t>(mn), slices);
     if (scale) total *= scale[i % n];
     C[i] = accumulate ? C[i] + total : total;
 }

@@ -46,19 +46,28 @@ __device__ __forceinline__ void widen4(uint32_t w, float* out) {
     out[3] = static_cast<float>(static_cast<int8_t>(w >> 24));
 }
 
-// Split-K arrival: every workgroup of a tile calls this after writing its
-// partial sums. It returns true (in all threads) only in the workgroup that
-// arrives last, which then sees every other workgroup's partials. The
-// device-scope fences write back and invalidate this XCD's L2 as the memory
-// model requires across XCDs; the counter is a plain vector atomic.
-__device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned arrivals, int* flag) {
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) *flag = atomicAdd(counter, 1u) == arrivals - 1u;
-    __syncthreads();
-    const bool last = *flag != 0;
-    if (last) __threadfence();
-    return last;
+// p[0] + p[stride] + ... + p[(slices - 1) * stride], added in slice order
+// (so every caller gets the same bits), with the loads issued 16 at a time
+// so the sum waits on one memory latency per 16 slices, not per slice.
+__device__ __forceinline__ float ordered_sum(const float* p, size_t stride, int slices) {
+    float total = 0.0f;
+    int s = 0;
+    for (; s + 16 <= slices; s += 16) {
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = p[static_cast<size_t>(s + i) * stride];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) total += v[i];
+    }
+    if (s < slices) {
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = s + i < slices ? p[static_cast<size_t>(s + i) * stride] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (s + i < slices) total += v[i];
+    }
+    return total;
 }
 
 __device__ __forceinline__ floatx4 mfma16x16x4(float a, float b, floatx4 c) {

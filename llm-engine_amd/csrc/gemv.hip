@@ -103,8 +103,6 @@ struct GemvParams {
     const BT* B;
     const float* scale;  // int8 only
     float* out;          // C when direct, else partials [slice][m][n]
-    float* C;            // final output (the fused reduction writes it)
-    unsigned* counters;  // per column tile; null: reduce_slices adds the slices
     int accumulate;
     int direct;
 };
@@ -143,13 +141,17 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
         a_reg[t] = (idx < MM * R && r < p.m && pp < p.k) ? p.A[r * p.k + pp] : 0.0f;
     }
 
-    // All L weight vectors of this lane in flight at once.
+    // All L weight vectors of this lane in flight at once. No load is
+    // predicated and no loaded value is selected, so nothing sits between a
+    // load and its use: a row past k reads row k - 1 (its A operand is
+    // staged as zero), and a lane past n reads column 0 (its sums are never
+    // stored). k * n < 2^31, so offsets are 32-bit from the uniform base.
+    const int lcol = active ? col : 0;
     V w[L];
 #pragma unroll
     for (int i = 0; i < L; ++i) {
-        const int pp = p0 + rg + i * E;
-        w[i] = (active && pp < p.k) ? LT::load(p.B + static_cast<size_t>(pp) * p.n + col)
-                                    : LT::zero();
+        const int pp = min(p0 + rg + i * E, p.k - 1);
+        w[i] = LT::load(p.B + static_cast<uint32_t>(pp * p.n + lcol));
     }
 
     if constexpr (NORM) {
@@ -223,27 +225,6 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
                 }
             }
             __syncthreads();
-        }
-    }
-
-    // Fused split-K: the last workgroup of this column tile adds the slices
-    // in slice order (so the bits do not depend on arrival order), applies
-    // the column scale and the residual, and re-arms the counter.
-    if (!p.direct && p.counters) {
-        __shared__ int last;
-        if (arrive_last(&p.counters[blockIdx.x], gridDim.y, &last)) {
-            if (c < p.n) {
-                const float s = kQ8 ? p.scale[c] : 1.0f;
-                for (int r = 0; r < p.m; ++r) {
-                    float total = 0.0f;
-                    for (int sl = 0; sl < static_cast<int>(gridDim.y); ++sl)
-                        total += p.out[(static_cast<size_t>(sl) * p.m + r) * p.n + c];
-                    float* o = p.C + static_cast<size_t>(r) * p.n + c;
-                    const float v = total * s;
-                    *o = p.accumulate ? *o + v : v;
-                }
-            }
-            if (tid == 0) p.counters[blockIdx.x] = 0u;
         }
     }
 }
@@ -350,17 +331,15 @@ void run_skinny(const MatmulArgs& a) {
     p.B = B;
     p.scale = a.scale;
     p.direct = slices == 1;
-    p.accumulate = a.accumulate;
-    p.C = a.C;
+    p.accumulate = a.accumulate && p.direct;
     p.out = p.direct ? a.C
                      : scratch(kPartial, static_cast<size_t>(slices) * a.m * a.n);
-    p.counters = (!p.direct && fused_reduce()) ? tile_counters(grid.x) : nullptr;
     if (a.rms_weight) {
         pick_width<BT, true>(E, L, p, grid, a.stream);
     } else {
         pick_width<BT, false>(E, L, p, grid, a.stream);
     }
-    if (!p.direct && !p.counters)
+    if (!p.direct)
         run_reduce_slices(a.m, a.n, slices, p.out,
                           std::is_same<BT, int8_t>::value ? a.scale : nullptr, a.C,
                           a.accumulate, a.stream);

@@ -30,15 +30,6 @@ enum ScratchSlot { kPartial = 0, kNorm = 1, kQuant = 2, kSlots = 3 };
 float* scratch(ScratchSlot slot, std::size_t floats);
 std::size_t scratch_generation();
 
-// Arrival counters for kernels whose last workgroup per column tile adds the
-// k slices itself. Zeroed when allocated; each such kernel's last workgroup
-// puts its counter back to zero, so they are zero between calls.
-unsigned* tile_counters(std::size_t count);
-
-// True unless EM_FUSED_REDUCE=0: split-K sums are added by the last
-// workgroup of each tile instead of a separate reduce_slices launch.
-bool fused_reduce();
-
 // Compute units of the current device (cached).
 int cu_count();
 

@@ -34,6 +34,7 @@ namespace {
 
 constexpr int kTile = 256;   // columns per workgroup
 constexpr int kChunk = 16;   // k rows per wave step
+constexpr int kTileStride = kTile + 4;  // LDS row stride of the epilogue tile
 
 template <class BT>
 struct SkParams {
@@ -48,6 +49,13 @@ struct SkParams {
 };
 
 // One chunk's B operands for one lane: four rows (u), 16 columns each.
+//
+// No load is predicated and no loaded value is selected: a lane whose
+// columns lie past n reads column 0 instead (its outputs are never stored),
+// and in the tail chunk of a slice a row past the slice end reads the
+// chunk's first row, whose product is cancelled by a zero A operand. The
+// main loop therefore has no branch or select between a load and its use,
+// so the wait before each multiply covers only that chunk's loads.
 template <class BT>
 struct BChunk;
 
@@ -56,15 +64,17 @@ struct BChunk<int8_t> {
     uint4 v[4];
     // Column of C (relative to the tile) that MFMA t reads in lane column j.
     static __device__ __forceinline__ int col(int j, int t) { return 16 * j + t; }
+    template <bool TAIL>
     __device__ __forceinline__ void load(const int8_t* B, int n, int k0row, int ke, int c0, int j,
                                          int g) {
-        const int c = c0 + 16 * j;
+        int c = c0 + 16 * j;
+        c = c < n ? c : 0;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int r = k0row + 4 * g + u;
-            v[u] = (r < ke && c < n)
-                       ? *reinterpret_cast<const uint4*>(B + static_cast<size_t>(r) * n + c)
-                       : make_uint4(0, 0, 0, 0);
+            int r = k0row + 4 * g + u;
+            if constexpr (TAIL) r = r < ke ? r : k0row;
+            // k * n < 2^31, so the offset fits 32 bits: base in SGPRs + VGPR offset.
+            v[u] = *reinterpret_cast<const uint4*>(B + static_cast<uint32_t>(r * n + c));
         }
     }
     __device__ __forceinline__ void widen(int u, float* b) const {
@@ -79,17 +89,18 @@ template <>
 struct BChunk<float> {
     float4 v[4][4];
     static __device__ __forceinline__ int col(int j, int t) { return 64 * (t >> 2) + 4 * j + (t & 3); }
+    template <bool TAIL>
     __device__ __forceinline__ void load(const float* B, int n, int k0row, int ke, int c0, int j,
                                          int g) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int r = k0row + 4 * g + u;
+            int r = k0row + 4 * g + u;
+            if constexpr (TAIL) r = r < ke ? r : k0row;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int c = c0 + 64 * q + 4 * j;
-                v[u][q] = (r < ke && c < n)
-                              ? *reinterpret_cast<const float4*>(B + static_cast<size_t>(r) * n + c)
-                              : make_float4(0.f, 0.f, 0.f, 0.f);
+                int c = c0 + 64 * q + 4 * j;
+                c = c < n ? c : 0;
+                v[u][q] = *reinterpret_cast<const float4*>(B + static_cast<uint32_t>(r * n + c));
             }
         }
     }
@@ -104,23 +115,28 @@ struct BChunk<float> {
     }
 };
 
-// AVEC: k % 4 == 0 and A 16-byte aligned, so a lane's four A values of a
-// chunk are one float4.
-template <class BT, int RB, bool AVEC>
-__device__ __forceinline__ void load_a(const float* A, int m, int k, int m0, int k0row, int j,
-                                       int g, floatx4 (&a)[RB]) {
+// A operands of one chunk: lane (g, j) holds A[m0 + 16 rb + j][k0 + 4g + u]
+// for u = 0..3, one float4 when AVEC (k % 4 == 0 and A 16-byte aligned).
+// Rows past m read row 0 (their outputs are never stored). In the tail
+// chunk, k past the slice end gives 0, which also cancels the clamped B rows.
+template <class BT, int RB, bool AVEC, bool TAIL>
+__device__ __forceinline__ void load_a(const float* A, int m, int k, int m0, int k0row, int ke,
+                                       int j, int g, floatx4 (&a)[RB]) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-        const int row = m0 + 16 * rb + j;
+        int row = m0 + 16 * rb + j;
+        row = row < m ? row : 0;
         const int kk = k0row + 4 * g;
-        if constexpr (AVEC) {
-            a[rb] = (row < m && kk < k)
-                        ? *reinterpret_cast<const floatx4*>(A + static_cast<size_t>(row) * k + kk)
-                        : floatx4{0.f, 0.f, 0.f, 0.f};
+        const float* src = A + static_cast<uint32_t>(row * k);
+        if constexpr (AVEC && !TAIL) {
+            a[rb] = *reinterpret_cast<const floatx4*>(src + kk);
         } else {
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
-                a[rb][u] = (row < m && kk + u < k) ? A[static_cast<size_t>(row) * k + kk + u] : 0.0f;
+            for (int u = 0; u < 4; ++u) {
+                const bool ok = !TAIL || kk + u < ke;
+                const float x = src[ok ? kk + u : k0row];
+                a[rb][u] = ok ? x : 0.0f;
+            }
         }
     }
 }
@@ -128,11 +144,14 @@ __device__ __forceinline__ void load_a(const float* A, int m, int k, int m0, int
 template <class BT, int RB, bool AVEC>
 __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(SkParams<BT> p) {
     constexpr bool kQ8 = std::is_same<BT, int8_t>::value;
-    // Waves 1..3 leave one row block's sums here: [wave-1][t][r][lane].
-    __shared__ float red[3 * 16 * 4 * kWave];
+    // Each wave's sums for one 16-row block, row-major by actual column.
+    __shared__ __attribute__((aligned(16))) float tile[4 * 16 * kTileStride];
 
     const int tid = threadIdx.x;
-    const int lane = tid % kWave, w = tid / kWave;
+    const int lane = tid % kWave;
+    // The wave index is uniform across the wave; saying so keeps every loop
+    // test below a scalar branch.
+    const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int g = lane >> 4, j = lane & 15;
     const int c0 = blockIdx.x * kTile;
     const int m0 = blockIdx.z * 16 * RB;
@@ -145,80 +164,104 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(SkParams<BT> p) {
 #pragma unroll
         for (int t = 0; t < 16; ++t) acc[rb][t] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    int k0 = kb + kChunk * w;
-    BChunk<BT> bc;
-    floatx4 a[RB];
-    if (k0 < ke) {
-        bc.load(p.B, p.n, k0, ke, c0, j, g);
-        load_a<BT, RB, AVEC>(p.A, p.m, p.k, m0, k0, j, g, a);
-    }
-    for (; k0 < ke; k0 += 4 * kChunk) {
-        BChunk<BT> bn;
-        floatx4 an[RB];
-        const int k1 = k0 + 4 * kChunk;
-        if (k1 < ke) {
-            bn.load(p.B, p.n, k1, ke, c0, j, g);
-            load_a<BT, RB, AVEC>(p.A, p.m, p.k, m0, k1, j, g, an);
-        }
+    // Full 16-row chunks, ping-ponging over two register sets: chunk i is
+    // multiplied while chunk i + 1 loads into the other set, with no copies
+    // between them. Then at most one partial chunk at the end of the slice.
+    // Row u + 1 is widened while row u's MFMAs run (two register sets), and
+    // the scheduler is asked to alternate MFMA and VALU, so no MFMA waits on
+    // a conversion it just issued.
+    auto multiply = [&](const BChunk<BT>& bc, const floatx4 (&a)[RB]) {
+        float bx[2][16];
+        bc.widen(0, bx[0]);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            float b[16];
-            bc.widen(u, b);
+            if (u + 1 < 4) bc.widen(u + 1, bx[(u + 1) & 1]);
 #pragma unroll
             for (int t = 0; t < 16; ++t)
 #pragma unroll
-                for (int rb = 0; rb < RB; ++rb) acc[rb][t] = mfma16x16x4(a[rb][u], b[t], acc[rb][t]);
+                for (int rb = 0; rb < RB; ++rb)
+                    acc[rb][t] = mfma16x16x4(a[rb][u], bx[u & 1][t], acc[rb][t]);
         }
-        bc = bn;
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) a[rb] = an[rb];
+        for (int i = 0; i < 64; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, RB, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);   // VALU
+        }
+    };
+    constexpr int kStep = 4 * kChunk;  // the four waves' chunks
+    int k0 = kb + kChunk * w;
+    BChunk<BT> b0, b1;
+    floatx4 a0[RB], a1[RB];
+    // The scheduling barrier keeps the compiler from sinking the prefetch
+    // down to its use (which it does to lower register pressure).
+    auto fetch = [&](BChunk<BT>& bc, floatx4 (&a)[RB], int at) {
+        load_a<BT, RB, AVEC, false>(p.A, p.m, p.k, m0, at, ke, j, g, a);
+        bc.template load<false>(p.B, p.n, at, ke, c0, j, g);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // Full chunks of this wave: k0 + i * kStep for i < nfull. They are
+    // multiplied in pairs with one exit at the bottom of the loop, so every
+    // path into the loop head has the same loads in flight and each
+    // multiply waits only for its own chunk. Past the last chunk the
+    // prefetch re-reads it (a cache hit) instead of branching.
+    const int nfull = ke - k0 >= kChunk ? (ke - k0 - kChunk) / kStep + 1 : 0;
+    auto at = [&](int i) { return k0 + (i < nfull ? i : nfull - 1) * kStep; };
+    if (nfull > 0) {
+        fetch(b0, a0, at(0));
+        for (int i = 0; i + 1 < nfull; i += 2) {
+            fetch(b1, a1, at(i + 1));
+            multiply(b0, a0);
+            fetch(b0, a0, at(i + 2));
+            multiply(b1, a1);
+        }
+        if (nfull & 1) multiply(b0, a0);
+    }
+    k0 += nfull * kStep;
+    if (k0 < ke) {  // the slice's last, partial chunk
+        load_a<BT, RB, AVEC, true>(p.A, p.m, p.k, m0, k0, ke, j, g, a0);
+        b0.template load<true>(p.B, p.n, k0, ke, c0, j, g);
+        multiply(b0, a0);
     }
 
-    // Wave sums, added in wave order: acc(0) + acc(1) + acc(2) + acc(3).
+    // Epilogue, one 16-row block at a time: every wave stores its sums in
+    // LDS as a row-major 16 x 256 tile (by actual column), then each thread
+    // takes 16 consecutive columns of one row, adds the four waves in wave
+    // order and writes four float4: consecutive threads write consecutive
+    // 64-byte runs. (Writing straight from the MFMA layout would scatter
+    // 4-byte stores 64 bytes apart.)
+    const int orow = tid / 16, ocol = (tid % 16) * 16;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-        if (w > 0) {
+        if (rb > 0) __syncthreads();  // the previous block's tile has been read
+        float* mine = tile + w * 16 * kTileStride;
 #pragma unroll
-            for (int t = 0; t < 16; ++t)
+        for (int t = 0; t < 16; ++t) {
+            const int c = BChunk<BT>::col(j, t);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) red[(((w - 1) * 16 + t) * 4 + r) * kWave + lane] = acc[rb][t][r];
+            for (int r = 0; r < 4; ++r) mine[(4 * g + r) * kTileStride + c] = acc[rb][t][r];
         }
         __syncthreads();
-        if (w == 0) {
+        const int row = m0 + 16 * rb + orow;
+        if (row < p.m) {
 #pragma unroll
-            for (int ww = 0; ww < 3; ++ww)
+            for (int q = 0; q < 4; ++q) {
+                const int c = c0 + ocol + 4 * q;
+                if (c >= p.n) break;
+                floatx4 v = *reinterpret_cast<const floatx4*>(&tile[orow * kTileStride + ocol + 4 * q]);
 #pragma unroll
-                for (int t = 0; t < 16; ++t)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[rb][t][r] += red[((ww * 16 + t) * 4 + r) * kWave + lane];
-        }
-        __syncthreads();
-    }
-    if (w != 0) return;
-
-    // Lane (g, j) holds rows m0 + 16 rb + 4g + r and columns c0 + col(j, t).
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {
-        const int c = c0 + BChunk<BT>::col(j, t);
-        if (c >= p.n) continue;
-        float s = 1.0f;
-        if constexpr (kQ8) {
-            if (p.direct) s = p.scale[c];
-        }
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = m0 + 16 * rb + 4 * g + r;
-                if (row >= p.m) continue;
-                const float v = acc[rb][t][r] * s;
+                for (int ww = 1; ww < 4; ++ww)
+                    v += *reinterpret_cast<const floatx4*>(
+                        &tile[(ww * 16 + orow) * kTileStride + ocol + 4 * q]);
                 if (p.direct) {
-                    float* o = p.out + static_cast<size_t>(row) * p.n + c;
+                    if constexpr (kQ8) v *= *reinterpret_cast<const floatx4*>(p.scale + c);
+                    floatx4* o = reinterpret_cast<floatx4*>(p.out + static_cast<size_t>(row) * p.n + c);
                     *o = p.accumulate ? *o + v : v;
                 } else {
-                    p.out[(static_cast<size_t>(blockIdx.y) * p.m + row) * p.n + c] = v;
+                    *reinterpret_cast<floatx4*>(
+                        p.out + (static_cast<size_t>(blockIdx.y) * p.m + row) * p.n + c) = v;
                 }
             }
+        }
     }
 }
 
