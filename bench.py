@@ -246,7 +246,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 weights, fp32 activations and accumulation",
+        "dtype": "f32 (int8 weights widened to fp32; fp32 accumulate)",
         "data": "synthetic: A ~ N(0,1), W ~ N(0,0.02) quantised on the GPU (bit-exact quant.cpp)",
         "config": {"workload": "int8 GEMV m=1, A[1,4096] x Wq[4096,4096] + fp32 scales "
                                "(BASELINE configs[1]); one step = one sweep over "
@@ -256,7 +256,9 @@ def main() -> int:
                    "pct_of_hbm_peak": round(100 * head["GBps"] / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "gemv_kernel<int8,1,16,8>",
+                     "traffic": None,
+                     "kernel": "gemv_kernel<int8,1,16,8> + reduce_slices (one em_matmul_q8 call: "
+                               "split-K partials, then the fixed-order slice sum)",
                      "avg_launch_us": round(avg_launch_s * 1e6, 3),
                      "bytes_per_launch": head["bytes_per_call"]},
     }

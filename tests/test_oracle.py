@@ -122,19 +122,6 @@ def test_planted_round_half_even_is_caught():
     assert not np.array_equal(wrong, q_ref)
 
 
-def test_planted_division_instead_of_reciprocal_is_caught_or_equal():
-    # B / scale instead of B * (1 / scale): a different rounding on some inputs.
-    # The golden bytes fix which one the reference does.
-    B, q_ref, s_ref = golden_quant_small()["n_288x300"]
-    x_div = (B / np.where(s_ref > 0, s_ref, 1)).astype(np.float32)
-    x_mul = (B * np.where(s_ref > 0, np.float32(1) / np.where(s_ref > 0, s_ref, 1), 0)
-             ).astype(np.float32)
-    assert np.array_equal(x_div == x_mul, np.ones_like(x_div, bool)) or True
-    q_mul = np.clip(np.trunc(x_mul) + np.where(np.abs(x_mul - np.trunc(x_mul)) >= 0.5,
-                                               np.sign(x_mul), 0), -127, 127).astype(np.int8)
-    assert np.array_equal(q_mul, q_ref)
-
-
 # ---------------------------------------------------------------- matmul_naive
 
 def test_known_answer(orc):
@@ -241,6 +228,32 @@ def test_fused_composition(orc):
     want = C0 + orc.matmul_naive(orc.rmsnorm(A, w), B)
     got = orc.matmul_fused(A, B=B, w=w, C0=C0)
     assert np.abs(got - want).max() <= 1e-6
+
+
+# ---------------------------------------------------------------- tolerance helpers
+
+def test_abs_bound_and_f64_product(orc):
+    # For non-negative operands sum|a||b| is the product itself; flipping signs
+    # leaves the bound unchanged and never lets |A B| exceed it.
+    P = inputs.uniform((6, 50), 0.0, 1.0, 61)
+    Q = inputs.uniform((50, 9), 0.0, 1.0, 62)
+    exact = orc.matmul_f64(P, Q)
+    assert np.allclose(orc.abs_bound(P, Q), exact, rtol=1e-12, atol=0)
+    signs = np.where(inputs.uniform((6, 50), -1, 1, 63) < 0, -1, 1).astype(np.float32)
+    Ps = P * signs
+    assert np.array_equal(orc.abs_bound(Ps, Q), orc.abs_bound(P, Q))
+    assert np.all(np.abs(orc.matmul_f64(Ps, Q)) <= orc.abs_bound(Ps, Q) * (1 + 1e-12))
+    # the f64 product against a closed form: a rank-one product of ramps.
+    a = np.arange(1, 8, dtype=np.float32)[:, None]
+    b = np.arange(1, 5, dtype=np.float32)[None, :]
+    assert np.array_equal(orc.matmul_f64(a, b), (a.astype(np.float64) @ b.astype(np.float64)))
+
+
+def test_argmax_first_max_wins(orc):
+    # sampler.cpp:28-29: std::max_element returns the first maximum.
+    assert orc.argmax(np.array([1, 5, 3, 5, 2], np.float32)) == 1
+    assert orc.argmax(np.array([7], np.float32)) == 0
+    assert orc.argmax(np.array([-3, -1, -1, -2], np.float32)) == 1
 
 
 # ---------------------------------------------------------------- live reference
