@@ -49,8 +49,10 @@ struct TiledParams {
 
 // VEC: k % 4 == 0, n % 4 == 0 and both operands aligned for 16-byte (fp32 B)
 // or 4-byte (int8 B) vector loads. Otherwise every element is loaded alone.
+// Four workgroups per CU (at most 128 registers): the 1024 tiles of an
+// N = 4096 product are then all resident at once, with no tail wave.
 template <class BT, bool VEC>
-__global__ __launch_bounds__(kThreads) void gemm_tiled_kernel(TiledParams<BT> p) {
+__global__ __launch_bounds__(kThreads, 4) void gemm_tiled_kernel(TiledParams<BT> p) {
     constexpr bool kQ8 = std::is_same<BT, int8_t>::value;
     __shared__ __attribute__((aligned(16))) float As[2][BM * AST];
     __shared__ __attribute__((aligned(16))) float Bs[2][BK * BST];
@@ -76,14 +78,6 @@ __global__ __launch_bounds__(kThreads) void gemm_tiled_kernel(TiledParams<BT> p)
         b_row[h] = f >> 5;
         b_cq[h] = (f & 31) * 4;
     }
-    float bscale[2][4];
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int c = n0 + b_cq[h] + e;
-            bscale[h][e] = (kQ8 && c < p.n) ? p.scale[c] : 1.0f;
-        }
 
     floatx4 ra[2], rb[2];
     auto fetch = [&](int k0) {
@@ -108,13 +102,17 @@ __global__ __launch_bounds__(kThreads) void gemm_tiled_kernel(TiledParams<BT> p)
             if constexpr (VEC) {
                 const bool ok = row_ok && gc < p.n;
                 if constexpr (kQ8) {
+                    // Column scales are re-read per slab (an L1 hit) rather than
+                    // held in registers, to stay within 128 registers.
                     const uint32_t w =
                         ok ? *reinterpret_cast<const uint32_t*>(p.B + static_cast<size_t>(gk) * p.n + gc)
                            : 0u;
+                    const floatx4 sc = gc < p.n ? *reinterpret_cast<const floatx4*>(p.scale + gc)
+                                                : floatx4{0.f, 0.f, 0.f, 0.f};
                     float v[4];
                     widen4(w, v);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) rb[h][e] = v[e] * bscale[h][e];
+                    for (int e = 0; e < 4; ++e) rb[h][e] = v[e] * sc[e];
                 } else {
                     rb[h] = ok ? *reinterpret_cast<const floatx4*>(p.B + static_cast<size_t>(gk) * p.n + gc)
                                : floatx4{0.f, 0.f, 0.f, 0.f};
@@ -125,7 +123,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tiled_kernel(TiledParams<BT> p)
                     const bool ok = row_ok && gc + e < p.n;
                     const size_t idx = static_cast<size_t>(gk) * p.n + gc + e;
                     if constexpr (kQ8) {
-                        rb[h][e] = ok ? static_cast<float>(p.B[idx]) * bscale[h][e] : 0.0f;
+                        rb[h][e] = ok ? static_cast<float>(p.B[idx]) * p.scale[gc + e] : 0.0f;
                     } else {
                         rb[h][e] = ok ? p.B[idx] : 0.0f;
                     }
@@ -196,7 +194,8 @@ __global__ __launch_bounds__(kThreads) void gemm_tiled_kernel(TiledParams<BT> p)
 
 bool vec_ok(const MatmulArgs& a, size_t b_align) {
     return a.k % 4 == 0 && a.n % 4 == 0 && reinterpret_cast<uintptr_t>(a.A) % 16 == 0 &&
-           reinterpret_cast<uintptr_t>(a.B) % b_align == 0;
+           reinterpret_cast<uintptr_t>(a.B) % b_align == 0 &&
+           (a.scale == nullptr || reinterpret_cast<uintptr_t>(a.scale) % 16 == 0);
 }
 
 }  // namespace
