@@ -114,8 +114,7 @@ def time_graph(torch, graph, steps: int, warmup: int):
     return start.elapsed_time(end) / 1e3, wall
 
 
-def gemv_case(em, torch, m, q8, steps, warmup, copies=None, seed=1000):
-    k = n = DIM
+def gemv_case(em, torch, m, q8, steps, warmup, copies=None, seed=1000, k=DIM, n=DIM):
     per_copy = k * n * (1 if q8 else 4)
     copies = copies or max(2, -(-POOL_MIN_BYTES // per_copy))
     pool = Pool(em, torch, q8, k, n, copies, seed)
@@ -134,6 +133,51 @@ def gemv_case(em, torch, m, q8, steps, warmup, copies=None, seed=1000):
     del graph, pool
     torch.cuda.synchronize()
     return out, (A, C)
+
+
+# Config 5: Llama-7B layer projections (in x out), int8 weights.
+LLAMA7B_LAYER = [("wq", 4096, 4096), ("wk", 4096, 4096), ("wv", 4096, 4096), ("wo", 4096, 4096),
+                 ("w1", 4096, 11008), ("w3", 4096, 11008), ("w2", 11008, 4096)]
+
+
+def llama7b_case(em, torch, steps):
+    """Per-projection and whole-layer times at decode (m = 1, cache-cold
+    rotating pools, graph replay) and prefill (m = 512, events over reps)."""
+    out = {"decode_m1": {}, "prefill_m512": {}}
+    times1, times512 = {}, {}
+    for k, n in sorted({(k, n) for _, k, n in LLAMA7B_LAYER} | {(4096, 32000)}):
+        r, _ = gemv_case(em, torch, 1, True, max(4, steps // 4), 2, seed=50, k=k, n=n)
+        times1[(k, n)] = r["us_per_call"]
+        W = torch.randn((k, n), device="cuda") * 0.02
+        q, s = em.quantize_q8(W)
+        del W
+        A = torch.randn((512, k), device="cuda")
+        C = torch.empty((512, n), device="cuda")
+        for _ in range(2):
+            em.matmul(A, q, C, scale=s)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 10
+        e0.record()
+        for _ in range(reps):
+            em.matmul(A, q, C, scale=s)
+        e1.record()
+        torch.cuda.synchronize()
+        times512[(k, n)] = e0.elapsed_time(e1) / reps * 1e3
+        del q, s, A, C
+    for name, k, n in LLAMA7B_LAYER + [("cls", 4096, 32000)]:
+        t1, t5 = times1[(k, n)], times512[(k, n)]
+        out["decode_m1"][name] = {"us": round(t1, 2),
+                                  "GBps": round(gemv_bytes(1, k, n, True) / t1 / 1e3, 1)}
+        out["prefill_m512"][name] = {"us": round(t5, 1),
+                                     "TFLOPS": round(2 * 512 * k * n / t5 / 1e6, 1)}
+    out["decode_m1"]["layer_us"] = round(sum(times1[(k, n)] for _, k, n in LLAMA7B_LAYER), 1)
+    out["prefill_m512"]["layer_us"] = round(sum(times512[(k, n)] for _, k, n in LLAMA7B_LAYER), 1)
+    layer_bytes = sum(gemv_bytes(1, k, n, True) for _, k, n in LLAMA7B_LAYER)
+    layer_flops = sum(2 * 512 * k * n for _, k, n in LLAMA7B_LAYER)
+    out["decode_m1"]["layer_GBps"] = round(layer_bytes / out["decode_m1"]["layer_us"] / 1e3, 1)
+    out["prefill_m512"]["layer_TFLOPS"] = round(layer_flops / out["prefill_m512"]["layer_us"] / 1e6, 1)
+    return out
 
 
 def host_median_convention(em, torch, A, w, s, C, reps=101):
@@ -282,6 +326,7 @@ def main() -> int:
         gemm, gemm_AB = gemm_case(em, torch)
         extra["fp32_gemm_N4096"] = {k: round(v, 3) if isinstance(v, float) else v
                                     for k, v in gemm.items()}
+        extra["llama7b_layer_int8"] = llama7b_case(em, torch, steps)
         # The reference's own convention (bench_cuda.cpp:41-54): host time of
         # one launch -> synchronize, median of 101, one W (cache-resident).
         pool = Pool(em, torch, True, DIM, DIM, 1, 99)

@@ -272,6 +272,29 @@ def test_config1_fp32_gemv_4096():
     check(got, orc.matmul_naive(A, W), A, W, 4096)
 
 
+# Config 5: Llama-7B layer projections, int8 (quantised on the GPU), decode
+# m = 1 (every element checked) and prefill m = 512 (rows sampled against
+# the f64 product and the 1e-4 * sum|a||w| bound). (k, n) = (in, out).
+LLAMA7B = {"wq": (4096, 4096), "w1": (4096, 11008), "w2": (11008, 4096), "cls": (4096, 32000)}
+
+
+@pytest.mark.parametrize("name", sorted(LLAMA7B))
+def test_config5_llama7b_projections(name):
+    k, n = LLAMA7B[name]
+    W = inputs.normal((k, n), 0.02, 5000 + k + n)
+    q, s = em.quantize_q8(dev(W))
+    qh, sh = host(q), host(s)
+    Wd = orc.dequantize(qh, sh)
+    A1 = inputs.normal((1, k), 1.0, 6000 + n)
+    got1 = host(em.matmul(dev(A1), q, scale=s))
+    check(got1, orc.matmul_fused(A1, Bq=qh, scale=sh), A1, Wd, k)
+    A = inputs.normal((512, k), 1.0, 7000 + n)
+    got = host(em.matmul(dev(A), q, scale=s))
+    rows = np.array([0, 1, 77, 255, 256, 400, 510, 511])
+    exact = orc.matmul_f64(A[rows], Wd)
+    assert np.all(np.abs(got[rows] - exact) <= 1e-4 * orc.abs_bound(A[rows], Wd))
+
+
 @pytest.mark.parametrize("N", [1024, 2048, 4096])
 def test_config3_square_gemm(N):
     # Config 3: A, B ~ U(-1, 1) N x N on the MFMA GEMM. Full C against the
