@@ -2,6 +2,7 @@
 """Benchmark of the MI355X matmul hot path (BASELINE.json metric).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+    python bench.py --profile-pass      (eager launches for rocprofv3 --pmc)
 
 Workload (the metric's headline): int8-weight GEMV,
 m = 1, A[1, 4096] fp32 ~ N(0, 1) times W[4096, 4096] ~ N(0, 0.02) quantised
@@ -16,8 +17,10 @@ hide the kernel.
 
 value = algorithmic bytes (W + scales + A + C) x products / seconds, in GB/s.
 The JSON line also carries:
-  roofline     the GEMV kernel's bytes per launch / its average launch time
-               from HIP events over the timed region, against 8 TB/s HBM
+  roofline     the product's algorithmic bytes per call / its average call
+               time from HIP events over the timed region, against 8 TB/s
+               HBM; traffic = HBM bytes per call measured with FETCH_SIZE and
+               WRITE_SIZE (profiles/gemv_int8_m1_4096_traffic.json)
   cpu_baseline the reference's own matmul_parallel (oracle/_ref, built from
                /root/reference/src with amdclang++ -O3) on the box's host
                cores, same inputs, median as bench_matmul.cpp:49-63
@@ -215,6 +218,44 @@ def gemm_case(em, torch, N=4096, reps=20):
             "pct_of_fp32_mfma_peak": 100 * tflops / FP32_MFMA_PEAK_TFLOPS}, (A, B)
 
 
+CALIBRATION_BYTES = 256 << 20
+
+
+def profile_pass(em, torch, sweeps: int = 2) -> dict:
+    """Eager launches (one dispatch per kernel, no graph) for rocprofv3 counter
+    passes. First a plain elementwise copy of CALIBRATION_BYTES (torch.neg into
+    a second buffer: that many bytes read and as many written, each once), the
+    yardstick the HBM byte counters are scaled by; then the headline product
+    (int8 m = 1, 4096^2) over the rotating pool, `sweeps` times."""
+    src = torch.randn(CALIBRATION_BYTES // 4, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    per_copy = DIM * DIM
+    copies = -(-POOL_MIN_BYTES // per_copy)
+    pool = Pool(em, torch, True, DIM, DIM, copies, 1000)
+    A = torch.randn((1, DIM), device="cuda")
+    C = torch.empty((1, DIM), device="cuda")
+    for _ in range(sweeps):
+        for w, s in zip(pool.ws, pool.scales):
+            em.matmul(A, w, C, scale=s)
+    torch.cuda.synchronize()
+    return {"calibration_bytes": CALIBRATION_BYTES, "products": sweeps * copies,
+            "bytes_per_product": gemv_bytes(1, DIM, DIM, True)}
+
+
+def measured_traffic():
+    """HBM bytes per headline call from the committed counter summary, or None."""
+    path = os.path.join(ROOT, "profiles", "gemv_int8_m1_4096_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
 def cpu_threads() -> int:
     try:
         n = len(os.sched_getaffinity(0))
@@ -260,6 +301,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="eager launches for rocprofv3 --pmc (calibration copy + headline)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -273,12 +316,16 @@ def main() -> int:
     if not torch.cuda.is_available() or not em.available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
+    if args.profile_pass:
+        print(json.dumps(profile_pass(em, torch)))
+        return 0
 
     head, (A1, _) = gemv_case(em, torch, 1, True, args.steps, args.warmup)
     steps = args.steps
     secs = head["secs"]
     avg_launch_s = secs / head["calls"]
     achieved = head["bytes_per_call"] / avg_launch_s / 1e9
+    traffic = measured_traffic()
     result = {
         "metric": METRIC,
         "value": round(head["GBps"], 1),
@@ -300,7 +347,9 @@ def main() -> int:
                    "pct_of_hbm_peak": round(100 * head["GBps"] / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": traffic["hbm_bytes_per_call"] if traffic else None,
+                     "traffic_note": (traffic["note"] if traffic else
+                                      "no counter summary in profiles/"),
                      "kernel": "gemv_kernel<int8,1,16,8> + reduce_slices (one em_matmul_q8 call: "
                                "split-K partials, then the fixed-order slice sum)",
                      "avg_launch_us": round(avg_launch_s * 1e6, 3),
