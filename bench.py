@@ -350,7 +350,7 @@ def main() -> int:
                      "traffic": traffic["hbm_bytes_per_call"] if traffic else None,
                      "traffic_note": (traffic["note"] if traffic else
                                       "no counter summary in profiles/"),
-                     "kernel": "gemv_kernel<int8,1,16,8> + reduce_slices (one em_matmul_q8 call: "
+                     "kernel": "gemv_kernel<int8,1,16,16> + reduce_slices (one em_matmul_q8 call: "
                                "split-K partials, then the fixed-order slice sum)",
                      "avg_launch_us": round(avg_launch_s * 1e6, 3),
                      "bytes_per_launch": head["bytes_per_call"]},

@@ -41,7 +41,7 @@ template <>
 struct Lane<int8_t, 16> {
     using V = uint4;
     static __device__ __forceinline__ V load(const int8_t* p) {
-        return *reinterpret_cast<const uint4*>(p);
+        return stream_load(reinterpret_cast<const uint4*>(p));
     }
     static __device__ __forceinline__ V zero() { return make_uint4(0, 0, 0, 0); }
     static __device__ __forceinline__ void widen(const V& v, float* b) {
@@ -56,7 +56,7 @@ template <>
 struct Lane<int8_t, 4> {
     using V = uint32_t;
     static __device__ __forceinline__ V load(const int8_t* p) {
-        return *reinterpret_cast<const uint32_t*>(p);
+        return stream_load(reinterpret_cast<const uint32_t*>(p));
     }
     static __device__ __forceinline__ V zero() { return 0u; }
     static __device__ __forceinline__ void widen(const V& v, float* b) { widen4(v, b); }
@@ -65,7 +65,7 @@ struct Lane<int8_t, 4> {
 template <>
 struct Lane<int8_t, 1> {
     using V = int8_t;
-    static __device__ __forceinline__ V load(const int8_t* p) { return *p; }
+    static __device__ __forceinline__ V load(const int8_t* p) { return stream_load(p); }
     static __device__ __forceinline__ V zero() { return 0; }
     static __device__ __forceinline__ void widen(const V& v, float* b) {
         b[0] = static_cast<float>(v);
@@ -76,7 +76,7 @@ template <>
 struct Lane<float, 4> {
     using V = float4;
     static __device__ __forceinline__ V load(const float* p) {
-        return *reinterpret_cast<const float4*>(p);
+        return stream_load(reinterpret_cast<const float4*>(p));
     }
     static __device__ __forceinline__ V zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
     static __device__ __forceinline__ void widen(const V& v, float* b) {
@@ -90,7 +90,7 @@ struct Lane<float, 4> {
 template <>
 struct Lane<float, 1> {
     using V = float;
-    static __device__ __forceinline__ V load(const float* p) { return *p; }
+    static __device__ __forceinline__ V load(const float* p) { return stream_load(p); }
     static __device__ __forceinline__ V zero() { return 0.f; }
     static __device__ __forceinline__ void widen(const V& v, float* b) { b[0] = v; }
 };
@@ -202,30 +202,30 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
     }
 
     // Add the E row groups in order, one row of C at a time. Thread t then
-    // owns local column t of the tile.
+    // owns local column t of the tile. Rows past m hold zeros and go through
+    // the same steps with their stores skipped: a branch on m around the
+    // barriers measured 0.6 us slower per 16 MiB GEMV.
     const int ccg = tid / E, cj = tid % E;
     const int c = blockIdx.x * kThreads + tid;
 #pragma unroll
     for (int r = 0; r < MM; ++r) {
-        if (r < p.m) {
 #pragma unroll
-            for (int j = 0; j < E; ++j) red[(rg * E + j) * RS + cg] = acc[r][j];
-            __syncthreads();
-            float total = 0.0f;
+        for (int j = 0; j < E; ++j) red[(rg * E + j) * RS + cg] = acc[r][j];
+        __syncthreads();
+        float total = 0.0f;
 #pragma unroll
-            for (int g = 0; g < E; ++g) total += red[(g * E + cj) * RS + ccg];
-            if (c < p.n) {
-                if (p.direct) {
-                    float v = total;
-                    if constexpr (kQ8) v *= p.scale[c];
-                    float* o = p.out + static_cast<size_t>(r) * p.n + c;
-                    *o = p.accumulate ? *o + v : v;
-                } else {
-                    p.out[(static_cast<size_t>(blockIdx.y) * p.m + r) * p.n + c] = total;
-                }
+        for (int g = 0; g < E; ++g) total += red[(g * E + cj) * RS + ccg];
+        if (r < p.m && c < p.n) {
+            if (p.direct) {
+                float v = total;
+                if constexpr (kQ8) v *= p.scale[c];
+                float* o = p.out + static_cast<size_t>(r) * p.n + c;
+                *o = p.accumulate ? *o + v : v;
+            } else {
+                p.out[(static_cast<size_t>(blockIdx.y) * p.m + r) * p.n + c] = total;
             }
-            __syncthreads();
         }
+        __syncthreads();
     }
 }
 
@@ -278,8 +278,11 @@ bool aligned(const void* ptr, size_t bytes) {
     return reinterpret_cast<uintptr_t>(ptr) % bytes == 0;
 }
 
-// Rows per lane: the deepest of 16 / 8 / 4 that still gives the grid about
-// two workgroups per CU (measured faster than one per CU at 4096^2).
+// Rows per lane: the deepest of 16 / 8 / 4 that still gives the grid half a
+// workgroup per CU or more. Deep slices mean fewer partials to reduce; with
+// nontemporal weight loads one 16-row-deep workgroup per CU streams a
+// 4096^2 int8 matrix faster than two 8-deep ones, and sweeps over the
+// Llama-7B and stories15M shapes put the cut near CUs / 2.
 // EM_GEMV_ROWS_PER_LANE overrides it (tuning sweeps).
 // The result is what the launched kernel uses: capped by max_depth as
 // pick_rows caps it.
@@ -296,7 +299,7 @@ int rows_per_lane(int E, int m, int n, int k) {
         L = forced;
     } else {
         const long long tiles = ceil_div(n, kThreads);
-        const long long target = 2LL * cu_count();
+        const long long target = cu_count() / 2;
         for (int depth : {16, 8}) {
             if (tiles * ceil_div(k, static_cast<long long>(E) * depth) >= target) {
                 L = depth;
