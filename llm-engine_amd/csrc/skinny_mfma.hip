@@ -34,6 +34,7 @@ namespace {
 
 constexpr int kTile = 256;   // columns per workgroup
 constexpr int kChunk = 16;   // k rows per wave step
+constexpr int kDepth = 2;    // chunks in flight per wave
 constexpr int kTileStride = kTile + 4;  // LDS row stride of the epilogue tile
 
 template <class BT>
@@ -74,7 +75,7 @@ struct BChunk<int8_t> {
             int r = k0row + 4 * g + u;
             if constexpr (TAIL) r = r < ke ? r : k0row;
             // k * n < 2^31, so the offset fits 32 bits: base in SGPRs + VGPR offset.
-            v[u] = *reinterpret_cast<const uint4*>(B + static_cast<uint32_t>(r * n + c));
+            v[u] = stream_load(reinterpret_cast<const uint4*>(B + static_cast<uint32_t>(r * n + c)));
         }
     }
     __device__ __forceinline__ void widen(int u, float* b) const {
@@ -100,7 +101,7 @@ struct BChunk<float> {
             for (int q = 0; q < 4; ++q) {
                 int c = c0 + 64 * q + 4 * j;
                 c = c < n ? c : 0;
-                v[u][q] = *reinterpret_cast<const float4*>(B + static_cast<uint32_t>(r * n + c));
+                v[u][q] = stream_load(reinterpret_cast<const float4*>(B + static_cast<uint32_t>(r * n + c)));
             }
         }
     }
@@ -164,63 +165,65 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(SkParams<BT> p) {
 #pragma unroll
         for (int t = 0; t < 16; ++t) acc[rb][t] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    // Full 16-row chunks, ping-ponging over two register sets: chunk i is
-    // multiplied while chunk i + 1 loads into the other set, with no copies
-    // between them. Then at most one partial chunk at the end of the slice.
-    // Row u + 1 is widened while row u's MFMAs run (two register sets), and
-    // the scheduler is asked to alternate MFMA and VALU, so no MFMA waits on
-    // a conversion it just issued.
+    // Row u + 1 of a chunk is widened while row u's MFMAs run. Each MFMA is
+    // paired with one conversion for the next row and a scheduling barrier
+    // pins that order: left to itself the scheduler puts every conversion
+    // right before the MFMA that reads it, and each MFMA then waits on it
+    // (measured 1.2x slower at m = 16).
     auto multiply = [&](const BChunk<BT>& bc, const floatx4 (&a)[RB]) {
         float bx[2][16];
         bc.widen(0, bx[0]);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            if (u + 1 < 4) bc.widen(u + 1, bx[(u + 1) & 1]);
+            float next[16];
+            if (u + 1 < 4) bc.widen(u + 1, next);
 #pragma unroll
-            for (int t = 0; t < 16; ++t)
+            for (int t = 0; t < 16; ++t) {
 #pragma unroll
                 for (int rb = 0; rb < RB; ++rb)
                     acc[rb][t] = mfma16x16x4(a[rb][u], bx[u & 1][t], acc[rb][t]);
-        }
-#pragma unroll
-        for (int i = 0; i < 64; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, RB, 0);  // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);   // VALU
+                if (u + 1 < 4) bx[(u + 1) & 1][t] = next[t];
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     };
     constexpr int kStep = 4 * kChunk;  // the four waves' chunks
     int k0 = kb + kChunk * w;
-    BChunk<BT> b0, b1;
-    floatx4 a0[RB], a1[RB];
-    // The scheduling barrier keeps the compiler from sinking the prefetch
+    // The scheduling barrier keeps the compiler from sinking a prefetch
     // down to its use (which it does to lower register pressure).
     auto fetch = [&](BChunk<BT>& bc, floatx4 (&a)[RB], int at) {
         load_a<BT, RB, AVEC, false>(p.A, p.m, p.k, m0, at, ke, j, g, a);
         bc.template load<false>(p.B, p.n, at, ke, c0, j, g);
         __builtin_amdgcn_sched_barrier(0);
     };
-    // Full chunks of this wave: k0 + i * kStep for i < nfull. They are
-    // multiplied in pairs with one exit at the bottom of the loop, so every
-    // path into the loop head has the same loads in flight and each
-    // multiply waits only for its own chunk. Past the last chunk the
-    // prefetch re-reads it (a cache hit) instead of branching.
+    // Full chunks of this wave are k0 + i * kStep for i < nfull, kept in a
+    // ring of kDepth register sets: all kDepth are in flight before the
+    // first multiply, and each multiply is followed by the load of the
+    // chunk kDepth ahead into the set it frees. Past the last chunk the
+    // ring re-reads it (a cache hit) rather than branch around a load, so
+    // every multiply waits only for its own chunk's loads. Then at most
+    // one partial chunk at the end of the slice.
     const int nfull = ke - k0 >= kChunk ? (ke - k0 - kChunk) / kStep + 1 : 0;
     auto at = [&](int i) { return k0 + (i < nfull ? i : nfull - 1) * kStep; };
+    BChunk<BT> b[kDepth];
+    floatx4 a[kDepth][RB];
     if (nfull > 0) {
-        fetch(b0, a0, at(0));
-        for (int i = 0; i + 1 < nfull; i += 2) {
-            fetch(b1, a1, at(i + 1));
-            multiply(b0, a0);
-            fetch(b0, a0, at(i + 2));
-            multiply(b1, a1);
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) fetch(b[d], a[d], at(d));
+        for (int i = 0; i < nfull; i += kDepth) {
+#pragma unroll
+            for (int d = 0; d < kDepth; ++d) {
+                if (i + d < nfull) multiply(b[d], a[d]);
+                fetch(b[d], a[d], at(i + d + kDepth));
+            }
         }
-        if (nfull & 1) multiply(b0, a0);
     }
     k0 += nfull * kStep;
     if (k0 < ke) {  // the slice's last, partial chunk
-        load_a<BT, RB, AVEC, true>(p.A, p.m, p.k, m0, k0, ke, j, g, a0);
-        b0.template load<true>(p.B, p.n, k0, ke, c0, j, g);
-        multiply(b0, a0);
+        load_a<BT, RB, AVEC, true>(p.A, p.m, p.k, m0, k0, ke, j, g, a[0]);
+        b[0].template load<true>(p.B, p.n, k0, ke, c0, j, g);
+        multiply(b[0], a[0]);
     }
 
     // Epilogue, one 16-row block at a time: every wave stores its sums in
@@ -295,10 +298,12 @@ void run_tiled_split(const MatmulArgs& a) {
     const int RB = a.m <= 16 ? 1 : 2;
     const int row_tiles = ceil_div(a.m, 16 * RB);
     const int col_tiles = ceil_div(a.n, kTile);
-    // Split k until the grid has about two workgroups per CU, keeping every
-    // slice at least 256 rows deep (four 16-row chunks per wave).
+    // Split k until the grid has about one workgroup per CU, keeping every
+    // slice at least 256 rows deep (four 16-row chunks per wave). More
+    // slices measured slower: each adds m x n partials to write and re-read
+    // (at m = 64, 16 slices move as many partial bytes as the int8 weights).
     const long long blocks = static_cast<long long>(row_tiles) * col_tiles;
-    const int want = std::max(1, ceil_div(2LL * cu_count(), blocks));
+    const int want = std::max(1, ceil_div(static_cast<long long>(cu_count()), blocks));
     int slices = std::max(1, std::min(want, ceil_div(a.k, 256)));
     const int span = ceil_div(ceil_div(a.k, slices), 4 * kChunk) * 4 * kChunk;
     slices = ceil_div(a.k, span);
