@@ -36,10 +36,10 @@ extern "C" {
 #define EM_ENODEV 3  /* no usable GPU */
 
 /* Kernel choice; replaces enum class GpuKernel, cuda_matmul.h:61-67. */
-#define EM_KERNEL_AUTOMATIC 0   /* skinny for m <= 8, tiled_split up to 64, tiled beyond */
+#define EM_KERNEL_AUTOMATIC 0   /* skinny for m <= 8, else tiled_split (tiled if B is unaligned) */
 #define EM_KERNEL_NAIVE 1       /* one thread per element of C; the reference kernel */
 #define EM_KERNEL_TILED 2       /* LDS-tiled fp32 MFMA GEMM, 128 x 128 tiles */
-#define EM_KERNEL_TILED_SPLIT 3 /* MFMA over 16/32/64-row tiles, B streamed once, k split */
+#define EM_KERNEL_TILED_SPLIT 3 /* MFMA over 16/32-row tiles, B streamed from HBM/L2, k split */
 #define EM_KERNEL_SKINNY 4      /* m <= 8 only: wave64 GEMV, k split across waves and blocks */
 
 #define EM_STREAM_PER_THREAD ((void*)2) /* hipStreamPerThread */

@@ -204,11 +204,19 @@ template <class BT>
 void run_tiled(const MatmulArgs& a) {
     const int tiles_n = ceil_div(a.n, BN), tiles_m = ceil_div(a.m, BM);
     const long long tiles = static_cast<long long>(tiles_n) * tiles_m;
-    // Split k when the tile grid leaves most CUs idle and k is deep enough
-    // for each slice to keep 256+ rows.
+    // Split k when the tile grid gives fewer than two workgroups per CU and
+    // k is deep enough for each slice to keep 256+ rows (two per CU measured
+    // 1.2-1.3x faster than one on the Llama-7B m = 512 projections, and four
+    // no better). EM_TILED_BLOCKS_PER_CU overrides the target (tuning sweeps).
+    static const int per_cu = [] {
+        const char* v = std::getenv("EM_TILED_BLOCKS_PER_CU");
+        const int x = v ? std::atoi(v) : 0;
+        return x > 0 ? x : 2;
+    }();
     int slices = 1;
-    if (tiles < cu_count()) {
-        const int want = ceil_div(cu_count(), tiles);
+    const long long target = static_cast<long long>(per_cu) * cu_count();
+    if (tiles < target) {
+        const int want = ceil_div(target, tiles);
         slices = std::max(1, std::min(want, a.k / 256));
     }
     const int span = ceil_div(ceil_div(a.k, slices), BK) * BK;

@@ -24,6 +24,7 @@
 //  * int8 sums stay unscaled; the column scale is applied to the reduced
 //    sum (direct) or after the slices are added (reduce_slices).
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "common.hpp"
@@ -47,7 +48,39 @@ struct SkParams {
     float* out;  // C (direct) or partials [slice][m][n]
     int accumulate;
     int direct;
+    int row_tiles, col_tiles;  // grid = row_tiles * col_tiles * slices workgroups
+    int xcd_order;
 };
+
+// Tile of workgroup `id` of a 1-D grid. Workgroups are dispatched to the
+// eight XCDs in turn (id % 8), each XCD with its own L2. With xcd_order the
+// ids are renumbered so that each XCD receives a contiguous run of tiles,
+// row tile fastest: the row tiles that stream the same 256 columns of B run
+// side by side on one XCD and share its L2, instead of landing on eight
+// different L2s. The renumbering is a bijection for any grid size.
+struct TileId {
+    int row, col, slice;
+};
+__device__ __forceinline__ TileId tile_of(int id, int total, int row_tiles, int col_tiles,
+                                          bool xcd_order) {
+    constexpr int kXcds = 8;
+    int idx = id;
+    if (xcd_order) {
+        const int per = total / kXcds, rem = total % kXcds;
+        const int x = id % kXcds, seq = id / kXcds;
+        idx = (x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per) + seq;
+        TileId t;
+        t.row = idx % row_tiles;
+        t.col = (idx / row_tiles) % col_tiles;
+        t.slice = idx / (row_tiles * col_tiles);
+        return t;
+    }
+    TileId t;
+    t.col = idx % col_tiles;
+    t.slice = (idx / col_tiles) % (total / (row_tiles * col_tiles));
+    t.row = idx / (total / row_tiles);
+    return t;
+}
 
 // One chunk's B operands for one lane: four rows (u), 16 columns each.
 //
@@ -154,9 +187,11 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(SkParams<BT> p) {
     // test below a scalar branch.
     const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int g = lane >> 4, j = lane & 15;
-    const int c0 = blockIdx.x * kTile;
-    const int m0 = blockIdx.z * 16 * RB;
-    const int kb = blockIdx.y * p.k_span;
+    const int total = gridDim.x;
+    const TileId place = tile_of(blockIdx.x, total, p.row_tiles, p.col_tiles, p.xcd_order != 0);
+    const int c0 = place.col * kTile;
+    const int m0 = place.row * 16 * RB;
+    const int kb = place.slice * p.k_span;
     const int ke = min(p.k, kb + p.k_span);
 
     floatx4 acc[RB][16];
@@ -261,7 +296,7 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(SkParams<BT> p) {
                     *o = p.accumulate ? *o + v : v;
                 } else {
                     *reinterpret_cast<floatx4*>(
-                        p.out + (static_cast<size_t>(blockIdx.y) * p.m + row) * p.n + c) = v;
+                        p.out + (static_cast<size_t>(place.slice) * p.m + row) * p.n + c) = v;
                 }
             }
         }
@@ -298,12 +333,15 @@ void run_tiled_split(const MatmulArgs& a) {
     const int RB = a.m <= 16 ? 1 : 2;
     const int row_tiles = ceil_div(a.m, 16 * RB);
     const int col_tiles = ceil_div(a.n, kTile);
-    // Split k until the grid has about one workgroup per CU, keeping every
+    // Split k until the grid has up to one workgroup per CU, keeping every
     // slice at least 256 rows deep (four 16-row chunks per wave). More
     // slices measured slower: each adds m x n partials to write and re-read
     // (at m = 64, 16 slices move as many partial bytes as the int8 weights).
+    // Rounding down keeps a grid just past the CU count from running a
+    // second, mostly idle round (m = 96: 288 workgroups took 1.25x as long
+    // as 240).
     const long long blocks = static_cast<long long>(row_tiles) * col_tiles;
-    const int want = std::max(1, ceil_div(static_cast<long long>(cu_count()), blocks));
+    const int want = static_cast<int>(std::max(1LL, cu_count() / blocks));
     int slices = std::max(1, std::min(want, ceil_div(a.k, 256)));
     const int span = ceil_div(ceil_div(a.k, slices), 4 * kChunk) * 4 * kChunk;
     slices = ceil_div(a.k, span);
@@ -319,7 +357,14 @@ void run_tiled_split(const MatmulArgs& a) {
     p.direct = slices == 1;
     p.accumulate = a.accumulate && p.direct;
     p.out = p.direct ? a.C : scratch(kPartial, static_cast<size_t>(slices) * a.m * a.n);
-    const dim3 grid(col_tiles, slices, row_tiles);
+    p.row_tiles = row_tiles;
+    p.col_tiles = col_tiles;
+    static const int xcd_env = [] {
+        const char* v = std::getenv("EM_XCD_ORDER");
+        return v ? std::atoi(v) : 1;
+    }();
+    p.xcd_order = xcd_env;
+    const dim3 grid(col_tiles * slices * row_tiles);
     const bool avec = a.k % 4 == 0 && reinterpret_cast<uintptr_t>(a.A) % 16 == 0;
     if (RB == 1) {
         launch<BT, 1>(p, grid, avec, a.stream);
