@@ -73,28 +73,61 @@ __global__ __launch_bounds__(kThreads) void fill_zero_kernel(float* p, size_t co
 
 // --- quantize_q8 -----------------------------------------------------------
 
-// Column maxima of |B| over one slice of rows: partial[slice][c].
+// Column maxima of |B| over one slice of rows: partial[slice][c]. With V4
+// (cols % 4 == 0, B 16-byte aligned) a thread owns four adjacent columns
+// and reads them as one float4; eight rows are loaded before any is used.
+template <bool V4>
 __global__ __launch_bounds__(kThreads) void colmax_kernel(int rows, int cols, int span,
                                                           const float* B, float* partial) {
-    const int c = blockIdx.x * kThreads + threadIdx.x;
+    constexpr int W = V4 ? 4 : 1;
+    const int c = (blockIdx.x * kThreads + threadIdx.x) * W;
     if (c >= cols) return;
     const int r0 = blockIdx.y * span, r1 = min(rows, r0 + span);
-    float mx = 0.0f;
     // fmaxf keeps the running value when |B| is NaN, as std::max(scale, v)
     // does in quant.cpp:14; on ordered values max is exact in any order.
-    for (int r = r0; r < r1; ++r) mx = fmaxf(mx, fabsf(B[static_cast<size_t>(r) * cols + c]));
-    partial[static_cast<size_t>(blockIdx.y) * cols + c] = mx;
+    float mx[W];
+#pragma unroll
+    for (int e = 0; e < W; ++e) mx[e] = 0.0f;
+    auto take = [&](int r) {
+        const float* row = B + static_cast<size_t>(r) * cols + c;
+        if constexpr (V4) {
+            const float4 v = *reinterpret_cast<const float4*>(row);
+            mx[0] = fmaxf(mx[0], fabsf(v.x));
+            mx[1] = fmaxf(mx[1], fabsf(v.y));
+            mx[2] = fmaxf(mx[2], fabsf(v.z));
+            mx[3] = fmaxf(mx[3], fabsf(v.w));
+        } else {
+            mx[0] = fmaxf(mx[0], fabsf(*row));
+        }
+    };
+    int r = r0;
+    for (; r + 8 <= r1; r += 8) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) take(r + u);
+    }
+    for (; r < r1; ++r) take(r);
+#pragma unroll
+    for (int e = 0; e < W; ++e) partial[static_cast<size_t>(blockIdx.y) * cols + c + e] = mx[e];
 }
 
 // scale[c] = absmax / 127 and inv[c] = 1 / scale (0 for a zero column), both
-// correctly rounded (the library is built with IEEE fp32 division).
+// correctly rounded (the library is built with IEEE fp32 division). The
+// slice maxima are loaded 16 at a time (max is exact in any order).
 __global__ __launch_bounds__(kThreads) void scale_kernel(int cols, int slices,
                                                          const float* partial, float* scale,
                                                          float* inv) {
     const int c = blockIdx.x * kThreads + threadIdx.x;
     if (c >= cols) return;
     float mx = 0.0f;
-    for (int s = 0; s < slices; ++s) mx = fmaxf(mx, partial[static_cast<size_t>(s) * cols + c]);
+    int s = 0;
+    for (; s + 16 <= slices; s += 16) {
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = partial[static_cast<size_t>(s + i) * cols + c];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, v[i]);
+    }
+    for (; s < slices; ++s) mx = fmaxf(mx, partial[static_cast<size_t>(s) * cols + c]);
     const float sc = mx / 127.0f;
     scale[c] = sc;
     inv[c] = sc > 0.0f ? 1.0f / sc : 0.0f;
@@ -109,15 +142,34 @@ __device__ __forceinline__ float round_half_away(float x) {
     return fabsf(x - t) >= 0.5f ? t + copysignf(1.0f, x) : t;
 }
 
-// total < 2^31 (checked by the entry point), so int indices suffice.
+__device__ __forceinline__ int8_t quantize_one(float b, float inv) {
+#pragma clang fp contract(off)
+    const float x = b * inv;
+    const float r = fminf(fmaxf(round_half_away(x), -127.0f), 127.0f);
+    return static_cast<int8_t>(static_cast<int>(r));
+}
+
+// total < 2^31 (checked by the entry point), so int indices suffice. With
+// V4 (cols % 4 == 0, B 16-byte and q 4-byte aligned) a thread takes four
+// consecutive elements of one row: one float4 load and one 32-bit store.
+template <bool V4>
 __global__ __launch_bounds__(kThreads) void quantize_kernel(int total, int cols, const float* B,
                                                             const float* inv, int8_t* q) {
-#pragma clang fp contract(off)
-    for (int i = blockIdx.x * kThreads + threadIdx.x; i < total; i += gridDim.x * kThreads) {
-        const int c = i % cols;
-        const float x = B[i] * inv[c];
-        const float r = fminf(fmaxf(round_half_away(x), -127.0f), 127.0f);
-        q[i] = static_cast<int8_t>(static_cast<int>(r));
+    if constexpr (V4) {
+        const int quads = total / 4;
+        for (int i = blockIdx.x * kThreads + threadIdx.x; i < quads; i += gridDim.x * kThreads) {
+            const int c = (4 * i) % cols;
+            const float4 b = reinterpret_cast<const float4*>(B)[i];
+            const float4 s = *reinterpret_cast<const float4*>(inv + c);
+            const uint32_t w = static_cast<uint8_t>(quantize_one(b.x, s.x)) |
+                               static_cast<uint32_t>(static_cast<uint8_t>(quantize_one(b.y, s.y))) << 8 |
+                               static_cast<uint32_t>(static_cast<uint8_t>(quantize_one(b.z, s.z))) << 16 |
+                               static_cast<uint32_t>(static_cast<uint8_t>(quantize_one(b.w, s.w))) << 24;
+            reinterpret_cast<uint32_t*>(q)[i] = w;
+        }
+    } else {
+        for (int i = blockIdx.x * kThreads + threadIdx.x; i < total; i += gridDim.x * kThreads)
+            q[i] = quantize_one(B[i], inv[i % cols]);
     }
 }
 
@@ -165,8 +217,10 @@ void run_fill_zero(float* p, size_t count, hipStream_t stream) {
 
 void run_quantize_q8(int rows, int cols, const float* B, int8_t* q, float* scale,
                      hipStream_t stream) {
+    const bool v4 = cols % 4 == 0 && reinterpret_cast<uintptr_t>(B) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(q) % 4 == 0;
     // Enough row slices for ~4 workgroups per CU over the column tiles.
-    const int tiles = ceil_div(cols, kThreads);
+    const int tiles = ceil_div(cols, kThreads * (v4 ? 4 : 1));
     const int want = ceil_div(4LL * cu_count(), tiles);
     const int slices = rows ? std::max(1, std::min(want, ceil_div(rows, 16))) : 1;
     const int span = rows ? ceil_div(rows, slices) : 0;
@@ -174,17 +228,27 @@ void run_quantize_q8(int rows, int cols, const float* B, int8_t* q, float* scale
     float* work = scratch(kQuant, static_cast<size_t>(used) * cols + cols);
     float* inv = work + static_cast<size_t>(used) * cols;
     if (rows) {
-        hipLaunchKernelGGL(colmax_kernel, dim3(tiles, used), dim3(kThreads), 0, stream, rows, cols,
-                           span, B, work);
+        if (v4) {
+            hipLaunchKernelGGL(colmax_kernel<true>, dim3(tiles, used), dim3(kThreads), 0, stream,
+                               rows, cols, span, B, work);
+        } else {
+            hipLaunchKernelGGL(colmax_kernel<false>, dim3(tiles, used), dim3(kThreads), 0, stream,
+                               rows, cols, span, B, work);
+        }
     } else {
         run_fill_zero(work, cols, stream);
     }
-    hipLaunchKernelGGL(scale_kernel, dim3(tiles), dim3(kThreads), 0, stream, cols, used, work,
-                       scale, inv);
+    hipLaunchKernelGGL(scale_kernel, dim3(ceil_div(cols, kThreads)), dim3(kThreads), 0, stream,
+                       cols, used, work, scale, inv);
     const size_t total = static_cast<size_t>(rows) * cols;
-    if (total)
-        hipLaunchKernelGGL(quantize_kernel, dim3(grid_for(total)), dim3(kThreads), 0, stream,
-                           static_cast<int>(total), cols, B, inv, q);
+    if (total == 0) return;
+    if (v4) {
+        hipLaunchKernelGGL(quantize_kernel<true>, dim3(grid_for(total / 4)), dim3(kThreads), 0,
+                           stream, static_cast<int>(total), cols, B, inv, q);
+    } else {
+        hipLaunchKernelGGL(quantize_kernel<false>, dim3(grid_for(total)), dim3(kThreads), 0,
+                           stream, static_cast<int>(total), cols, B, inv, q);
+    }
 }
 
 void run_dequantize_q8(int rows, int cols, const int8_t* q, const float* scale, float* out,
