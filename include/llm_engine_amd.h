@@ -34,6 +34,7 @@ extern "C" {
 #define EM_EINVAL 1  /* bad arguments: shapes, kernel choice, sizes (std::invalid_argument) */
 #define EM_EDEVICE 2 /* a HIP runtime error (std::runtime_error "cuda: <op>: <err>") */
 #define EM_ENODEV 3  /* no usable GPU */
+#define EM_ERANGE 4  /* a token or position outside the model's range (std::out_of_range) */
 
 /* Kernel choice; replaces enum class GpuKernel, cuda_matmul.h:61-67. */
 #define EM_KERNEL_AUTOMATIC 0   /* skinny for m <= 8, else tiled_split (tiled if B is unaligned) */
@@ -96,6 +97,93 @@ int em_quantize_q8(size_t rows, size_t cols, const float* B, int8_t* q, float* s
  * quant.h:9, quant.cpp:30-36. */
 int em_dequantize_q8(size_t rows, size_t cols, const int8_t* q, const float* scale, float* out,
                      void* stream);
+
+/* ---- Causal attention over a KV cache (cuda_attention.h) ------------------ */
+
+/* Replaces struct AttentionShape, cuda_attention.h:8-13. */
+typedef struct {
+    int n_heads, n_kv_heads, head_size, seq_len;
+    size_t q_stride;   /* floats between rows of q; head h starts at h * head_size */
+    size_t kv_stride;  /* floats between positions of the caches (kv_dim) */
+    size_t out_stride; /* floats between rows of out */
+} em_attention_shape;
+
+/* Replaces enum class AttentionKernel, cuda_attention.h:15-19. */
+#define EM_ATTN_AUTOMATIC 0    /* split for up to 8 rows, single_block for more */
+#define EM_ATTN_SINGLE_BLOCK 1 /* one workgroup per (head, row), scores in LDS */
+#define EM_ATTN_SPLIT 2        /* positions split across workgroups, merged in chunk order */
+
+/* EM_OK if `kernel` can run shape s, else EM_EINVAL with the reason; replaces
+ * attention_check(), cuda_attention.h:23-26. Rejects a non-positive size,
+ * n_heads not a multiple of n_kv_heads, caches past 32-bit indexing; for split
+ * (and automatic) head_size or a stride not a multiple of 4; and a kernel whose
+ * LDS need (single_block: head_size + seq_len + 256 floats) passes 64 KiB. */
+int em_attention_check(const em_attention_shape* s, int kernel);
+
+/* Floats of scratch em_attention needs for `rows` rows (0 for single_block);
+ * replaces attention_scratch_floats(), cuda_attention.h:21-22. */
+size_t em_attention_scratch_floats(const em_attention_shape* s, size_t rows, int kernel);
+
+/* For each of `rows` rows and each query head h: row i sits at position
+ * *pos_dev + i and attends to cached positions [0, *pos_dev + i], with kv head
+ * h / (n_heads / n_kv_heads): out[i][h*head_size + d] =
+ * sum_t softmax_t(q . k_t / sqrt(head_size)) v_t[d]. pos_dev is device memory,
+ * so a captured graph serves every position; the caller keeps
+ * *pos_dev + rows <= seq_len. Replaces attention_cuda(), cuda_attention.h:28-38.
+ * Unlike the reference, scratch needs no zero fill (no counters), and results
+ * are bit-identical across calls. */
+int em_attention(const em_attention_shape* s, size_t rows, const int* pos_dev, const float* q,
+                 const float* key_cache, const float* value_cache, float* out, float* scratch,
+                 int kernel, void* stream);
+
+/* ---- The device-resident forward pass (cuda_model.h) --------------------- */
+
+/* Replaces struct Config, model.h:11-22: head_size = dim / n_heads,
+ * kv_dim = n_kv_heads * head_size. */
+typedef struct {
+    size_t dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len;
+} em_model_config;
+
+/* One layer's weights in the CPU model's layout (struct LayerWeights,
+ * model.h:29-36): projections stored in x out, row-major, host memory. */
+typedef struct {
+    const float* rms_att; /* dim */
+    const float* wqkv;    /* dim x (dim + 2 kv_dim): q | k | v */
+    const float* wo;      /* dim x dim */
+    const float* rms_ffn; /* dim */
+    const float* w13;     /* dim x 2 hidden_dim: gate (w1) | up (w3) */
+    const float* w2;      /* hidden_dim x dim */
+} em_layer_weights;
+
+/* Replaces enum class WeightType, model.h:60. q8 quantises every projection
+ * and the classifier with quantize_q8 (bit-exact with quant.cpp); the
+ * embedding stays fp32. */
+#define EM_WEIGHTS_F32 0
+#define EM_WEIGHTS_Q8 1
+
+typedef struct em_model em_model;
+
+/* Copies the weights to the GPU (quantising them there for q8) and allocates
+ * the KV cache. Replaces CudaTransformer(const Checkpoint&, WeightType),
+ * cuda_model.h:29-31. token_embedding is vocab_size x dim, rms_final dim,
+ * wcls dim x vocab_size (the CPU model's Weights, model.h:38-43); `layers`
+ * holds n_layers entries. EM_EINVAL for a shape the attention kernels cannot
+ * run (as the reference's constructor rejects one) or a NULL weight. */
+int em_model_create(const em_model_config* cfg, const float* token_embedding,
+                    const em_layer_weights* layers, const float* rms_final, const float* wcls,
+                    int weight_type, em_model** out);
+
+int em_model_destroy(em_model* m);
+
+/* Feeds tokens[0:n] at positions [pos, pos + n) and writes the logits of the
+ * token after the last (vocab_size floats, host memory). n == 1 is
+ * CudaTransformer::forward, n > 1 prefill (cuda_model.h:37-39); both wait for
+ * the GPU. EM_ERANGE (check_feed, model.cpp:165-177) for a token outside the
+ * vocabulary, pos + n > seq_len, or pos past the positions already fed;
+ * EM_EINVAL for n == 0. A rejected call leaves the cache as it was. The first
+ * one-token call is captured into a HIP graph that later ones replay. Not
+ * safe from several host threads at once. */
+int em_model_forward(em_model* m, const int* tokens, size_t n, size_t pos, float* logits);
 
 #ifdef __cplusplus
 }

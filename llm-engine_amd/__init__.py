@@ -20,7 +20,7 @@ from typing import Optional
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libllm_engine_amd.so")
 
-EM_OK, EM_EINVAL, EM_EDEVICE, EM_ENODEV = 0, 1, 2, 3
+EM_OK, EM_EINVAL, EM_EDEVICE, EM_ENODEV, EM_ERANGE = 0, 1, 2, 3, 4
 KERNELS = {"automatic": 0, "naive": 1, "tiled": 2, "tiled_split": 3, "skinny": 4}
 STREAM_PER_THREAD = 2
 
@@ -29,7 +29,29 @@ EXPORTS = (
     "em_last_error", "em_available", "em_synchronize", "em_scratch_generation",
     "em_malloc", "em_free", "em_memcpy_h2d", "em_memcpy_d2h",
     "em_matmul_f32", "em_matmul_q8", "em_quantize_q8", "em_dequantize_q8",
+    "em_attention_check", "em_attention_scratch_floats", "em_attention",
+    "em_model_create", "em_model_destroy", "em_model_forward",
 )
+ATTN_KERNELS = {"automatic": 0, "single_block": 1, "split": 2}
+
+
+class ModelConfig(ctypes.Structure):
+    """em_model_config (the reference's Config, model.h:11-22)."""
+    _fields_ = [(k, ctypes.c_size_t) for k in ("dim", "hidden_dim", "n_layers", "n_heads",
+                                                "n_kv_heads", "vocab_size", "seq_len")]
+
+
+class LayerWeights(ctypes.Structure):
+    """em_layer_weights (the reference's LayerWeights, model.h:29-36)."""
+    _fields_ = [(k, ctypes.c_void_p) for k in ("rms_att", "wqkv", "wo", "rms_ffn", "w13", "w2")]
+
+
+class AttentionShape(ctypes.Structure):
+    """em_attention_shape (the reference's AttentionShape, cuda_attention.h:8-13)."""
+    _fields_ = [("n_heads", ctypes.c_int), ("n_kv_heads", ctypes.c_int),
+                ("head_size", ctypes.c_int), ("seq_len", ctypes.c_int),
+                ("q_stride", ctypes.c_size_t), ("kv_stride", ctypes.c_size_t),
+                ("out_stride", ctypes.c_size_t)]
 
 
 class EngineError(Exception):
@@ -44,6 +66,10 @@ class InvalidArgument(EngineError, ValueError):
 
 class DeviceError(EngineError, RuntimeError):
     """EM_EDEVICE / EM_ENODEV: the reference's std::runtime_error."""
+
+
+class OutOfRange(EngineError, IndexError):
+    """EM_ERANGE: the reference's std::out_of_range (check_feed)."""
 
 
 _sz = ctypes.c_size_t
@@ -82,6 +108,16 @@ def lib() -> ctypes.CDLL:
                                    ctypes.c_int, _vp, _vp]
         L.em_quantize_q8.argtypes = [_sz, _sz, _vp, _vp, _vp, _vp]
         L.em_dequantize_q8.argtypes = [_sz, _sz, _vp, _vp, _vp, _vp]
+        shp = ctypes.POINTER(AttentionShape)
+        L.em_attention_check.argtypes = [shp, ctypes.c_int]
+        L.em_attention_scratch_floats.argtypes = [shp, _sz, ctypes.c_int]
+        L.em_attention_scratch_floats.restype = _sz
+        L.em_attention.argtypes = [shp, _sz, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_int, _vp]
+        L.em_model_create.argtypes = [ctypes.POINTER(ModelConfig), _vp,
+                                      ctypes.POINTER(LayerWeights), _vp, _vp, ctypes.c_int,
+                                      ctypes.POINTER(_vp)]
+        L.em_model_destroy.argtypes = [_vp]
+        L.em_model_forward.argtypes = [_vp, _vp, _sz, _sz, _vp]
         for name in EXPORTS:
             getattr(L, name).restype = getattr(L, name).restype or ctypes.c_int
         _lib = L
@@ -94,6 +130,8 @@ def _check(rc: int) -> None:
     msg = lib().em_last_error().decode()
     if rc == EM_EINVAL:
         raise InvalidArgument(rc, msg)
+    if rc == EM_ERANGE:
+        raise OutOfRange(rc, msg)
     raise DeviceError(rc, msg)
 
 
@@ -190,3 +228,88 @@ def dequantize_q8(q, scale, stream=None):
     dequantize_q8_raw(rows, cols, _dev(q, torch.int8), _dev(scale, torch.float32),
                       _dev(out, torch.float32), _stream_ptr(stream))
     return out
+
+
+# ---- attention ---------------------------------------------------------------
+
+def attention_shape(n_heads, n_kv_heads, head_size, seq_len, q_stride=None, kv_stride=None,
+                    out_stride=None) -> AttentionShape:
+    """The model's geometry by default: q rows strided like its qkv buffer."""
+    dim, kv = n_heads * head_size, n_kv_heads * head_size
+    return AttentionShape(n_heads, n_kv_heads, head_size, seq_len,
+                          dim + 2 * kv if q_stride is None else q_stride,
+                          kv if kv_stride is None else kv_stride,
+                          dim if out_stride is None else out_stride)
+
+
+def attention_check(shape: AttentionShape, kernel="automatic") -> None:
+    _check(lib().em_attention_check(ctypes.byref(shape), ATTN_KERNELS.get(kernel, kernel)))
+
+
+def attention_scratch_floats(shape: AttentionShape, rows: int, kernel="automatic") -> int:
+    return int(lib().em_attention_scratch_floats(ctypes.byref(shape), rows,
+                                                 ATTN_KERNELS.get(kernel, kernel)))
+
+
+def attention(shape: AttentionShape, rows: int, pos_dev, q, key_cache, value_cache, out=None,
+              scratch=None, kernel="automatic", stream=None):
+    """em_attention on torch tensors: pos_dev is a 1-element int32 device tensor."""
+    import torch
+    if out is None:
+        out = torch.empty((rows, shape.out_stride), dtype=torch.float32, device=q.device)
+    if scratch is None:
+        n = attention_scratch_floats(shape, rows, kernel)
+        scratch = torch.empty((max(1, n),), dtype=torch.float32, device=q.device)
+    _check(lib().em_attention(ctypes.byref(shape), rows, _dev(pos_dev, torch.int32),
+                              _dev(q, torch.float32), _dev(key_cache, torch.float32),
+                              _dev(value_cache, torch.float32), _dev(out, torch.float32),
+                              _dev(scratch, torch.float32), ATTN_KERNELS.get(kernel, kernel),
+                              _stream_ptr(stream)))
+    return out
+
+
+# ---- the forward pass --------------------------------------------------------
+
+class Model:
+    """em_model: the device-resident forward pass (the reference's
+    CudaTransformer, cuda_model.h:24-89). `weights` holds numpy fp32 arrays in
+    the CPU model's layout: token_embedding (vocab x dim), rms_final (dim),
+    wcls (dim x vocab) and `layers`, a list of dicts with rms_att, wqkv, wo,
+    rms_ffn, w13, w2 (projections in x out)."""
+
+    def __init__(self, config: dict, weights: dict, q8: bool = False):
+        import numpy as np
+        self.config = dict(config)
+        self._keep = []
+
+        def host(a):
+            a = np.ascontiguousarray(a, np.float32)
+            self._keep.append(a)
+            return a.ctypes.data
+
+        cfg = ModelConfig(**{k: int(config[k]) for k, _ in ModelConfig._fields_})
+        layers = (LayerWeights * len(weights["layers"]))()
+        for i, lw in enumerate(weights["layers"]):
+            layers[i] = LayerWeights(*(host(lw[k]) for k, _ in LayerWeights._fields_))
+        handle = _vp()
+        _check(lib().em_model_create(ctypes.byref(cfg), host(weights["token_embedding"]), layers,
+                                     host(weights["rms_final"]), host(weights["wcls"]),
+                                     int(bool(q8)), ctypes.byref(handle)))
+        self._keep = []  # the library has its own copies
+        self.h = handle.value
+
+    def forward(self, tokens, pos: int):
+        """Logits (vocab,) after feeding tokens at [pos, pos + len(tokens))."""
+        import numpy as np
+        t = np.ascontiguousarray(np.atleast_1d(tokens), np.int32)
+        out = np.empty((int(self.config["vocab_size"]),), np.float32)
+        _check(lib().em_model_forward(self.h, t.ctypes.data, t.size, pos, out.ctypes.data))
+        return out
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().em_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()

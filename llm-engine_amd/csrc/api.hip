@@ -21,20 +21,11 @@ namespace {
 
 thread_local std::string g_error;
 
-int fail(int code, const std::string& msg) {
-    g_error = msg;
-    return code;
-}
-
 std::mutex g_scratch_mu;
 float* g_scratch[kSlots] = {};
 std::size_t g_scratch_cap[kSlots] = {};
 std::atomic<std::size_t> g_generation{0};
 
-bool device_present() {
-    int count = 0;
-    return hipGetDeviceCount(&count) == hipSuccess && count > 0;
-}
 
 // a * b >= 2^31, without overflow: the kernels index with int
 // (cuda_matmul.cu:414-417).
@@ -119,6 +110,16 @@ int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, co
 }
 
 }  // namespace
+
+int fail(int code, const std::string& msg) {
+    g_error = msg;
+    return code;
+}
+
+bool device_present() {
+    int count = 0;
+    return hipGetDeviceCount(&count) == hipSuccess && count > 0;
+}
 
 float* scratch(ScratchSlot slot, std::size_t floats) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
@@ -255,6 +256,52 @@ int em_dequantize_q8(size_t rows, size_t cols, const int8_t* q, const float* sca
     try {
         em::run_dequantize_q8(static_cast<int>(rows), static_cast<int>(cols), q, scale, out,
                               static_cast<hipStream_t>(stream));
+        em::hip_check(hipGetLastError(), "launch");
+    } catch (const std::exception& e) {
+        return fail(EM_EDEVICE, e.what());
+    }
+    return EM_OK;
+}
+
+
+static em::AttnShape to_shape(const em_attention_shape& s) {
+    return {s.n_heads, s.n_kv_heads, s.head_size, s.seq_len, s.q_stride, s.kv_stride, s.out_stride};
+}
+
+int em_attention_check(const em_attention_shape* s, int kernel) {
+    if (!s) return fail(EM_EINVAL, "attention: null shape");
+    const std::string why = em::attention_reject(to_shape(*s), kernel);
+    return why.empty() ? EM_OK : fail(EM_EINVAL, why);
+}
+
+size_t em_attention_scratch_floats(const em_attention_shape* s, size_t rows, int kernel) {
+    if (!s || !em::attention_reject(to_shape(*s), kernel).empty()) return 0;
+    return em::attention_scratch_floats(to_shape(*s), rows, kernel);
+}
+
+int em_attention(const em_attention_shape* s, size_t rows, const int* pos_dev, const float* q,
+                 const float* key_cache, const float* value_cache, float* out, float* scratch,
+                 int kernel, void* stream) {
+    if (const int rc = em_attention_check(s, kernel)) return rc;
+    if (rows == 0) return EM_OK;
+    const em::AttnShape sh = to_shape(*s);
+    if (rows > static_cast<size_t>(sh.seq_len))
+        return fail(EM_EINVAL, "attention: more rows than seq_len");
+    if (too_many(rows, sh.q_stride) || too_many(rows, sh.out_stride))
+        return fail(EM_EINVAL, "attention: more than 2^31 elements");
+    if (!pos_dev || !q || !key_cache || !value_cache || !out)
+        return fail(EM_EINVAL, "attention: null pointer");
+    const bool split = em::attention_uses_split(sh, rows, kernel);
+    if (split) {
+        if (!scratch) return fail(EM_EINVAL, "attention: split needs scratch");
+        auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+        if (!a16(q) || !a16(key_cache) || !a16(value_cache) || !a16(out) || !a16(scratch))
+            return fail(EM_EINVAL, "attention: split needs 16-byte aligned q, caches, out, scratch");
+    }
+    if (!em::device_present()) return fail(EM_ENODEV, "attention: no usable GPU");
+    try {
+        em::run_attention(sh, static_cast<int>(rows), pos_dev, q, key_cache, value_cache, out,
+                          scratch, kernel, static_cast<hipStream_t>(stream));
         em::hip_check(hipGetLastError(), "launch");
     } catch (const std::exception& e) {
         return fail(EM_EDEVICE, e.what());

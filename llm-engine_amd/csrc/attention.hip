@@ -1,0 +1,398 @@
+// Causal attention over a KV cache, the step after the qkv projection of a
+// decode or prefill pass (reference: cuda_attention.h:8-39, attention_single
+// and attention_split in cuda_attention.cu:39-285, attention_cuda :339-362).
+//
+// Row i of a call sits at position *pos + i and attends to cached positions
+// [0, *pos + i]; query head h reads kv head h / (n_heads / n_kv_heads).
+// out[i][h*hs + d] = sum_t softmax_t(q . k_t / sqrt(hs)) v_t[d]. The position
+// is read on the device, so one captured graph serves every position.
+//
+// Two kernels, both for 256-thread workgroups of four wave64s:
+//
+//  * split (decode, few rows): workgroup (head group, row, chunk) scores one
+//    chunk of the context for the G query heads that share a kv head, so a
+//    key or value row is loaded once for all G. A position's key is read by
+//    a power-of-two group of lanes, float4 each, contiguous across the group,
+//    and the dot products are finished with xor shuffles inside the wave.
+//    The chunk's softmax is left unnormalised (max m, sum l, exp-weighted
+//    values o) in scratch, and a second kernel merges the chunks of each
+//    (row, head) in chunk order. The merge is a separate launch rather than a
+//    "last workgroup merges" arrival: on gfx950 every cross-workgroup arrival
+//    measured slower than a second launch, and the fixed merge order keeps
+//    results bit-identical across calls. A context that fits one chunk is
+//    normalised and written by the first kernel; the merge kernel then exits.
+//  * single_block (prefill, many rows): workgroup (head, row) holds the
+//    query and the scores of the whole context in LDS; any head size.
+//
+// The grid is sized for seq_len, never for the position: chunks past the end
+// of a row's context return at once.
+#include <cmath>
+#include <string>
+
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace em {
+namespace {
+
+constexpr int kMinChunk = 64;           // positions per split workgroup, at least
+constexpr int kMaxSplits = 256;         // chunks per (row, head group), at most
+constexpr std::size_t kSplitMaxRows = 8;   // automatic: split up to this many rows
+constexpr std::size_t kMaxLds = 64 * 1024;  // dynamic LDS per workgroup
+
+int split_count(int seq_len) {
+    const int s = (seq_len + kMinChunk - 1) / kMinChunk;
+    return s < kMaxSplits ? s : kMaxSplits;
+}
+
+__host__ __device__ __forceinline__ int chunk_size(int n_ctx, int splits) {
+    const int c = (n_ctx + splits - 1) / splits;
+    return c > kMinChunk ? c : kMinChunk;
+}
+
+int split_chunk_cap(const AttnShape& s) { return chunk_size(s.seq_len, split_count(s.seq_len)); }
+
+// Query heads per split workgroup: the most of 8, 4, 2, 1 that divides the
+// heads sharing a kv head.
+int heads_per_block(const AttnShape& s) {
+    const int group = s.n_heads / s.n_kv_heads;
+    for (int g : {8, 4, 2})
+        if (group % g == 0) return g;
+    return 1;
+}
+
+std::size_t single_lds(const AttnShape& s) {
+    return (static_cast<std::size_t>(s.head_size) + s.seq_len + kThreads) * sizeof(float);
+}
+
+std::size_t split_lds(const AttnShape& s) {
+    const std::size_t G = heads_per_block(s), hs = s.head_size;
+    const std::size_t cap4 = (static_cast<std::size_t>(split_chunk_cap(s)) + 3) / 4 * 4;
+    const std::size_t slots = kThreads / (hs / 4);
+    return (G * hs + G * cap4 + slots * G * hs) * sizeof(float);
+}
+
+struct SplitScratch {
+    std::size_t o, ml, total;  // offsets and size in floats
+};
+
+SplitScratch split_scratch(const AttnShape& s, std::size_t rows) {
+    const std::size_t blocks = rows * s.n_heads * split_count(s.seq_len);
+    auto up4 = [](std::size_t x) { return (x + 3) / 4 * 4; };
+    SplitScratch l{};
+    l.o = 0;
+    l.ml = up4(blocks * s.head_size);
+    l.total = l.ml + up4(2 * blocks);
+    return l;
+}
+
+int resolve(const AttnShape& s, int kernel, std::size_t rows) {
+    if (kernel != kAttnAutomatic) return kernel;
+    return rows <= kSplitMaxRows || single_lds(s) > kMaxLds ? kAttnSplit : kAttnSingle;
+}
+
+struct AttnArgs {
+    int n_heads, head_size, group, seq_len, splits, chunk_cap;
+    int q_stride, kv_stride, out_stride;
+    const int* pos;
+    const float* q;
+    const float* kc;
+    const float* vc;
+    float* part_o;
+    float2* part_ml;
+    float* out;
+};
+
+// Lanes per key row: hs4 rounded up to a power of two, at most one wave.
+__device__ __forceinline__ int lanes_per_row(int n) {
+    int l = 1;
+    while (l < n && l < kWave) l <<= 1;
+    return l;
+}
+
+template <int G>
+__global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
+    extern __shared__ floatx4 lds4[];
+    __shared__ float2 ml[G];
+    const int hs = a.head_size, hs4 = hs / 4;
+    const int cap4 = (a.chunk_cap + 3) / 4 * 4;
+    floatx4* q_s = lds4;                                    // G x hs4
+    float* sc = reinterpret_cast<float*>(q_s + G * hs4);    // G x cap4
+    floatx4* red = reinterpret_cast<floatx4*>(sc + G * cap4);  // slots x G x hs4
+
+    const int hg = blockIdx.x, i = blockIdx.y, s = blockIdx.z;
+    const int n_ctx = *a.pos + i + 1;
+    const int chunk = chunk_size(n_ctx, a.splits);
+    const int t0 = s * chunk;
+    if (t0 >= n_ctx) return;  // uniform across the workgroup
+    const int len = min(chunk, n_ctx - t0);
+    const int nchunks = (n_ctx + chunk - 1) / chunk;
+    const int h0 = hg * G;
+    const int kv_off = (h0 / a.group) * hs;
+    const int tid = threadIdx.x;
+
+    // The G heads are adjacent in the row of q.
+    const floatx4* qg = reinterpret_cast<const floatx4*>(
+        a.q + static_cast<std::size_t>(i) * a.q_stride + static_cast<std::size_t>(h0) * hs);
+    for (int j = tid; j < G * hs4; j += kThreads) q_s[j] = qg[j];
+    __syncthreads();
+
+    // Scores. Every lane runs the same trip count, so the shuffles see whole
+    // waves; lanes past the chunk contribute zeros and store nothing.
+    const int lpp = lanes_per_row(hs4);
+    const int sub = tid % lpp, slot = tid / lpp, nslots = kThreads / lpp;
+    const float scale = 1.0f / sqrtf(static_cast<float>(hs));
+    for (int base = 0; base < len; base += nslots) {
+        const int t = base + slot;
+        float dot[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) dot[g] = 0.0f;
+        if (t < len) {
+            const floatx4* k = reinterpret_cast<const floatx4*>(
+                a.kc + static_cast<std::size_t>(t0 + t) * a.kv_stride + kv_off);
+            for (int d = sub; d < hs4; d += lpp) {
+                const floatx4 kv = k[d];
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const floatx4 qv = q_s[g * hs4 + d];
+                    dot[g] += qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
+                }
+            }
+        }
+        for (int o = lpp / 2; o > 0; o >>= 1)
+#pragma unroll
+            for (int g = 0; g < G; ++g) dot[g] += __shfl_xor(dot[g], o, kWave);
+        if (t < len && sub == 0)
+#pragma unroll
+            for (int g = 0; g < G; ++g) sc[g * cap4 + t] = dot[g] * scale;
+    }
+    __syncthreads();
+
+    // The chunk's softmax, unnormalised: one wave per head.
+    const int lane = tid % kWave, wave = tid / kWave;
+    for (int g = wave; g < G; g += kThreads / kWave) {
+        float* row = sc + g * cap4;
+        float m = -INFINITY;
+        for (int t = lane; t < len; t += kWave) m = fmaxf(m, row[t]);
+        m = wave_max(m);
+        float l = 0.0f;
+        for (int t = lane; t < len; t += kWave) {
+            const float e = expf(row[t] - m);
+            row[t] = e;
+            l += e;
+        }
+        l = wave_sum(l);
+        if (lane == 0) ml[g] = make_float2(m, l);
+    }
+    __syncthreads();
+
+    // Weighted values: the hs4 threads of a slot read one value row as
+    // consecutive float4s; slots stride over positions and are added in LDS
+    // in slot order.
+    const int d4 = tid % hs4, r = tid / hs4, slots = kThreads / hs4;
+    if (r < slots) {
+        floatx4 acc[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) acc[g] = floatx4{0.f, 0.f, 0.f, 0.f};
+        const float* vb = a.vc + static_cast<std::size_t>(t0) * a.kv_stride + kv_off;
+        for (int t = r; t < len; t += slots) {
+            const floatx4 v =
+                reinterpret_cast<const floatx4*>(vb + static_cast<std::size_t>(t) * a.kv_stride)[d4];
+#pragma unroll
+            for (int g = 0; g < G; ++g) acc[g] += sc[g * cap4 + t] * v;
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) red[(r * G + g) * hs4 + d4] = acc[g];
+    }
+    __syncthreads();
+
+    const std::size_t head_row = static_cast<std::size_t>(i) * a.n_heads + h0;
+    for (int j = tid; j < G * hs4; j += kThreads) {
+        const int g = j / hs4, d = j % hs4;
+        floatx4 o = red[g * hs4 + d];
+        for (int rr = 1; rr < slots; ++rr) o += red[(rr * G + g) * hs4 + d];
+        if (nchunks == 1) {
+            const float inv = 1.0f / ml[g].y;
+            reinterpret_cast<floatx4*>(a.out + static_cast<std::size_t>(i) * a.out_stride +
+                                       static_cast<std::size_t>(h0 + g) * hs)[d] = o * inv;
+        } else {
+            reinterpret_cast<floatx4*>(a.part_o)[((head_row + g) * a.splits + s) * hs4 + d] = o;
+        }
+    }
+    if (nchunks > 1 && tid < G) a.part_ml[(head_row + tid) * a.splits + s] = ml[tid];
+}
+
+// Merges the chunks of one (head, row) in chunk order: m = max m_c,
+// l = sum e^(m_c - m) l_c, out = sum e^(m_c - m) o_c / l.
+__global__ __launch_bounds__(kWave) void attn_merge_kernel(AttnArgs a) {
+    const int h = blockIdx.x, i = blockIdx.y;
+    const int n_ctx = *a.pos + i + 1;
+    const int chunk = chunk_size(n_ctx, a.splits);
+    const int n = (n_ctx + chunk - 1) / chunk;
+    if (n == 1) return;  // written by the split kernel
+    const std::size_t b = (static_cast<std::size_t>(i) * a.n_heads + h) * a.splits;
+    float m = -INFINITY;
+    for (int c = 0; c < n; ++c) m = fmaxf(m, a.part_ml[b + c].x);
+    const int hs4 = a.head_size / 4;
+    const floatx4* po = reinterpret_cast<const floatx4*>(a.part_o);
+    floatx4* out = reinterpret_cast<floatx4*>(a.out + static_cast<std::size_t>(i) * a.out_stride +
+                                              static_cast<std::size_t>(h) * a.head_size);
+    for (int d = threadIdx.x; d < hs4; d += blockDim.x) {
+        float l = 0.0f;
+        floatx4 acc{0.f, 0.f, 0.f, 0.f};
+        for (int c = 0; c < n; ++c) {
+            const float2 p = a.part_ml[b + c];
+            const float w = expf(p.x - m);
+            l += w * p.y;
+            acc += w * po[(b + c) * hs4 + d];
+        }
+        out[d] = acc * (1.0f / l);
+    }
+}
+
+// One workgroup per (head, row): query and scores in LDS, scalar loads, so
+// any head size works.
+__global__ __launch_bounds__(kThreads) void attn_single_kernel(AttnArgs a) {
+    extern __shared__ float lds[];
+    __shared__ float part[4];
+    const int hs = a.head_size;
+    float* q_s = lds;               // hs
+    float* sc = lds + hs;           // seq_len
+    float* red = sc + a.seq_len;    // kThreads
+    const int h = blockIdx.x, i = blockIdx.y;
+    const int n_ctx = *a.pos + i + 1;
+    const int kv_off = (h / a.group) * hs;
+    const int tid = threadIdx.x;
+
+    const float* qg = a.q + static_cast<std::size_t>(i) * a.q_stride + static_cast<std::size_t>(h) * hs;
+    for (int d = tid; d < hs; d += kThreads) q_s[d] = qg[d];
+    __syncthreads();
+
+    const int lpp = lanes_per_row(hs);
+    const int sub = tid % lpp, slot = tid / lpp, nslots = kThreads / lpp;
+    const float scale = 1.0f / sqrtf(static_cast<float>(hs));
+    for (int base = 0; base < n_ctx; base += nslots) {
+        const int t = base + slot;
+        float dot = 0.0f;
+        if (t < n_ctx) {
+            const float* k = a.kc + static_cast<std::size_t>(t) * a.kv_stride + kv_off;
+            for (int d = sub; d < hs; d += lpp) dot += q_s[d] * k[d];
+        }
+        for (int o = lpp / 2; o > 0; o >>= 1) dot += __shfl_xor(dot, o, kWave);
+        if (t < n_ctx && sub == 0) sc[t] = dot * scale;
+    }
+    __syncthreads();
+
+    float m = -INFINITY;
+    for (int t = tid; t < n_ctx; t += kThreads) m = fmaxf(m, sc[t]);
+    m = block_max(m, part);
+    float l = 0.0f;
+    for (int t = tid; t < n_ctx; t += kThreads) {
+        const float e = expf(sc[t] - m);
+        sc[t] = e;
+        l += e;
+    }
+    l = block_sum(l, part);  // its barriers also publish the exponentials
+    const float inv = 1.0f / l;
+
+    float* oh = a.out + static_cast<std::size_t>(i) * a.out_stride + static_cast<std::size_t>(h) * hs;
+    const float* vb = a.vc + kv_off;
+    if (hs <= kThreads) {
+        const int d = tid % hs, r = tid / hs, slots = kThreads / hs;
+        if (r < slots) {
+            float acc = 0.0f;
+            for (int t = r; t < n_ctx; t += slots)
+                acc += sc[t] * vb[static_cast<std::size_t>(t) * a.kv_stride + d];
+            red[r * hs + d] = acc;
+        }
+        __syncthreads();
+        if (tid < hs) {
+            float o = red[tid];
+            for (int rr = 1; rr < slots; ++rr) o += red[rr * hs + tid];
+            oh[tid] = o * inv;
+        }
+    } else {
+        for (int d = tid; d < hs; d += kThreads) {
+            float acc = 0.0f;
+            for (int t = 0; t < n_ctx; ++t)
+                acc += sc[t] * vb[static_cast<std::size_t>(t) * a.kv_stride + d];
+            oh[d] = acc * inv;
+        }
+    }
+}
+
+template <int G>
+void launch_split(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t stream) {
+    const dim3 grid(s.n_heads / G, rows, a.splits);
+    hipLaunchKernelGGL((attn_split_kernel<G>), grid, dim3(kThreads), split_lds(s), stream, a);
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(s.n_heads, rows), dim3(kWave), 0, stream, a);
+}
+
+}  // namespace
+
+std::string attention_reject(const AttnShape& s, int kernel) {
+    if (kernel < kAttnAutomatic || kernel > kAttnSplit) return "attention: unknown kernel";
+    if (s.n_heads <= 0 || s.n_kv_heads <= 0 || s.head_size <= 0 || s.seq_len <= 0 ||
+        s.n_heads % s.n_kv_heads != 0)
+        return "attention: bad shape";
+    if (static_cast<std::size_t>(s.seq_len) * s.kv_stride >= (std::size_t{1} << 31) ||
+        s.q_stride >= (std::size_t{1} << 31) || s.out_stride >= (std::size_t{1} << 31))
+        return "attention: cache past 32-bit indexing";
+    const bool single = kernel == kAttnSingle;
+    // split loads float4s.
+    if (!single && (s.head_size % 4 || s.head_size > 4 * kThreads || s.q_stride % 4 ||
+                    s.kv_stride % 4 || s.out_stride % 4))
+        return "attention: split needs head_size and strides divisible by 4";
+    const std::size_t need = single ? single_lds(s) : split_lds(s);
+    if (need > kMaxLds)
+        return "attention: seq_len " + std::to_string(s.seq_len) + " needs " +
+               std::to_string(need) + " bytes of LDS, more than " + std::to_string(kMaxLds);
+    return "";
+}
+
+std::size_t attention_scratch_floats(const AttnShape& s, std::size_t rows, int kernel) {
+    if (kernel == kAttnSingle) return 0;
+    if (kernel == kAttnAutomatic && single_lds(s) <= kMaxLds)
+        rows = rows < kSplitMaxRows ? rows : kSplitMaxRows;
+    return split_scratch(s, rows).total;
+}
+
+bool attention_uses_split(const AttnShape& s, std::size_t rows, int kernel) {
+    return resolve(s, kernel, rows) == kAttnSplit;
+}
+
+void run_attention(const AttnShape& s, int rows, const int* pos, const float* q, const float* kc,
+                   const float* vc, float* out, float* scratch, int kernel, hipStream_t stream) {
+    kernel = resolve(s, kernel, rows);
+    AttnArgs a{};
+    a.n_heads = s.n_heads;
+    a.head_size = s.head_size;
+    a.group = s.n_heads / s.n_kv_heads;
+    a.seq_len = s.seq_len;
+    a.q_stride = static_cast<int>(s.q_stride);
+    a.kv_stride = static_cast<int>(s.kv_stride);
+    a.out_stride = static_cast<int>(s.out_stride);
+    a.pos = pos;
+    a.q = q;
+    a.kc = kc;
+    a.vc = vc;
+    a.out = out;
+    if (kernel == kAttnSingle) {
+        hipLaunchKernelGGL(attn_single_kernel, dim3(s.n_heads, rows), dim3(kThreads),
+                           single_lds(s), stream, a);
+        return;
+    }
+    const SplitScratch l = split_scratch(s, rows);
+    a.splits = split_count(s.seq_len);
+    a.chunk_cap = split_chunk_cap(s);
+    a.part_o = scratch + l.o;
+    a.part_ml = reinterpret_cast<float2*>(scratch + l.ml);
+    switch (heads_per_block(s)) {
+        case 8: launch_split<8>(s, a, rows, stream); break;
+        case 4: launch_split<4>(s, a, rows, stream); break;
+        case 2: launch_split<2>(s, a, rows, stream); break;
+        default: launch_split<1>(s, a, rows, stream); break;
+    }
+}
+
+}  // namespace em

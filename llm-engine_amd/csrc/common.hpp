@@ -43,6 +43,24 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Maximum over the 64 lanes of a wave.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+// Maximum over a 256-thread workgroup; every thread gets the result. `part`
+// is 4 floats of LDS; the leading barrier lets a previous call finish.
+__device__ __forceinline__ float block_max(float v, float* part) {
+    v = wave_max(v);
+    const int wave = threadIdx.x / kWave;
+    __syncthreads();
+    if ((threadIdx.x % kWave) == 0) part[wave] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+}
+
 // Sum over a 256-thread workgroup; every thread gets the result. The four
 // wave sums are added in wave order. `part` is 4 floats of LDS; the leading
 // barrier lets a previous call finish reading it.

@@ -83,4 +83,24 @@ void run_dequantize_q8(int rows, int cols, const int8_t* q, const float* scale, 
 
 inline int ceil_div(long long x, long long d) { return static_cast<int>((x + d - 1) / d); }
 
+// Records `msg` for em_last_error() on this thread and returns `code`.
+int fail(int code, const std::string& msg);
+bool device_present();
+
+// --- attention (attention.hip) ----------------------------------------------
+
+struct AttnShape {
+    int n_heads, n_kv_heads, head_size, seq_len;
+    std::size_t q_stride, kv_stride, out_stride;  // floats between rows / positions
+};
+enum AttnKernel { kAttnAutomatic = 0, kAttnSingle = 1, kAttnSplit = 2 };
+
+// "" if `kernel` can run shape `s`, else the reason.
+std::string attention_reject(const AttnShape& s, int kernel);
+std::size_t attention_scratch_floats(const AttnShape& s, std::size_t rows, int kernel);
+bool attention_uses_split(const AttnShape& s, std::size_t rows, int kernel);
+// Rows [0, rows) at positions *pos + i; the caller guarantees *pos + rows <= seq_len.
+void run_attention(const AttnShape& s, int rows, const int* pos, const float* q, const float* kc,
+                   const float* vc, float* out, float* scratch, int kernel, hipStream_t stream);
+
 }  // namespace em

@@ -62,6 +62,8 @@ class Oracle:
         lib.orc_matmul_f64.argtypes = [_sz, _sz, _sz, _f32p, _f32p, _f64p]
         lib.orc_argmax.argtypes = [_sz, _f32p]
         lib.orc_argmax.restype = _sz
+        lib.orc_attention.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, _sz, _sz, _f32p,
+                                      _sz, _f32p, _f32p, _sz, _f64p, _sz]
         self.lib = lib
 
     def quantize_q8(self, B):
@@ -135,6 +137,17 @@ class Oracle:
     def argmax(self, x) -> int:
         x = _f32(x).ravel()
         return int(self.lib.orc_argmax(x.size, _ptr(x, _f32p)))
+
+    def attention(self, n_heads, n_kv_heads, head_size, rows, pos, q, kc, vc):
+        """Double-precision causal attention; q is rows x q_stride, the caches
+        positions x kv_stride; returns rows x (n_heads * head_size) float64."""
+        q, kc, vc = _f32(q), _f32(kc), _f32(vc)
+        dim = n_heads * head_size
+        out = np.zeros((rows, dim), np.float64)
+        self.lib.orc_attention(n_heads, n_kv_heads, head_size, rows, pos, _ptr(q, _f32p),
+                               q.shape[1], _ptr(kc, _f32p), _ptr(vc, _f32p), kc.shape[1],
+                               _ptr(out, _f64p), dim)
+        return out
 
 
 def _cpu_has_avx512() -> bool:
@@ -269,3 +282,111 @@ def ref() -> Optional[Ref]:
         if os.path.exists(path):
             _ref = Ref(path)
     return _ref
+
+
+# ---- the reference's CPU model (oracle/_ref/libref_model.so) ----------------
+
+class RefCheckpoint:
+    """A checkpoint loaded by the reference's own loader (load_checkpoint,
+    model.cpp:115-163): config plus weights in the CPU model's layout."""
+
+    NAMES = ("token_embedding", "rms_final", "wcls")
+    LAYER_NAMES = ("rms_att", "wqkv", "wo", "rms_ffn", "w13", "w2")
+
+    def __init__(self, lib, path: str):
+        self.lib = lib
+        self.h = lib.ref_ckpt_load(path.encode())
+        if not self.h:
+            raise ValueError(lib.ref_model_error().decode())
+        cfg = (ctypes.c_size_t * 7)()
+        lib.ref_ckpt_config(self.h, cfg)
+        keys = ("dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads", "vocab_size", "seq_len")
+        self.config = dict(zip(keys, (int(x) for x in cfg)))
+
+    def array(self, name: str, layer: int = 0) -> np.ndarray:
+        n = int(self.lib.ref_ckpt_array(self.h, name.encode(), layer, None, 0))
+        out = np.empty((n,), np.float32)
+        self.lib.ref_ckpt_array(self.h, name.encode(), layer, _ptr(out, _f32p), n)
+        return out
+
+    def weights(self) -> dict:
+        c = self.config
+        D, H, V = c["dim"], c["hidden_dim"], c["vocab_size"]
+        KV = c["n_kv_heads"] * (D // c["n_heads"])
+        shapes = {"wqkv": (D, D + 2 * KV), "wo": (D, D), "w13": (D, 2 * H), "w2": (H, D)}
+        w = {"token_embedding": self.array("token_embedding").reshape(V, D),
+             "rms_final": self.array("rms_final"),
+             "wcls": self.array("wcls").reshape(D, V), "layers": []}
+        for l in range(c["n_layers"]):
+            w["layers"].append({k: (self.array(k, l).reshape(shapes[k]) if k in shapes
+                                    else self.array(k, l)) for k in self.LAYER_NAMES})
+        return w
+
+    def rope_tables(self):
+        c = self.config
+        half = c["dim"] // c["n_heads"] // 2
+        cos = np.empty((c["seq_len"] * half,), np.float32)
+        sin = np.empty_like(cos)
+        self.lib.ref_rope_tables(self.h, _ptr(cos, _f32p), _ptr(sin, _f32p))
+        return cos, sin
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.lib.ref_ckpt_free(self.h)
+            self.h = None
+
+
+class RefTransformer:
+    """The reference's CPU Transformer (model.h:79-108) over a RefCheckpoint."""
+
+    def __init__(self, lib, ckpt: RefCheckpoint, q8: bool):
+        self.lib, self.vocab = lib, ckpt.config["vocab_size"]
+        self.h = lib.ref_model_new(ckpt.h, int(q8))
+        if not self.h:
+            raise ValueError(lib.ref_model_error().decode())
+
+    def run(self, tokens, pos: int, single: bool = False) -> np.ndarray:
+        """prefill(tokens, pos), or forward(tokens[0], pos) when single."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = np.empty((self.vocab,), np.float32)
+        rc = self.lib.ref_model_run(self.h, t.ctypes.data_as(ctypes.POINTER(ctypes.c_int)),
+                                    t.size, pos, int(single), _ptr(out, _f32p))
+        if rc == 1:
+            raise IndexError(self.lib.ref_model_error().decode())
+        if rc:
+            raise ValueError(self.lib.ref_model_error().decode())
+        return out
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.lib.ref_model_free(self.h)
+            self.h = None
+
+
+_ref_model_lib = None
+
+
+def ref_model_lib():
+    """ctypes handle of oracle/_ref/libref_model.so, or None if not built."""
+    global _ref_model_lib
+    if _ref_model_lib is None:
+        path = os.path.join(HERE, "_ref", "libref_model.so")
+        if not os.path.exists(path):
+            return None
+        lib = ctypes.CDLL(path)
+        vp = ctypes.c_void_p
+        lib.ref_model_error.restype = ctypes.c_char_p
+        lib.ref_ckpt_load.restype = vp
+        lib.ref_ckpt_load.argtypes = [ctypes.c_char_p]
+        lib.ref_ckpt_free.argtypes = [vp]
+        lib.ref_ckpt_config.argtypes = [vp, ctypes.POINTER(ctypes.c_size_t)]
+        lib.ref_ckpt_array.restype = _sz
+        lib.ref_ckpt_array.argtypes = [vp, ctypes.c_char_p, _sz, _f32p, _sz]
+        lib.ref_model_new.restype = vp
+        lib.ref_model_new.argtypes = [vp, ctypes.c_int]
+        lib.ref_model_free.argtypes = [vp]
+        lib.ref_model_run.argtypes = [vp, ctypes.POINTER(ctypes.c_int), _sz, _sz, ctypes.c_int,
+                                      _f32p]
+        lib.ref_rope_tables.argtypes = [vp, _f32p, _f32p]
+        _ref_model_lib = lib
+    return _ref_model_lib

@@ -16,6 +16,9 @@
  *   orc_abs_bound        sum_k |a_ik| |b_kj| in double
  *                        1e-4 * sum|a||w| is built from it
  *   orc_matmul_f64       double-accumulated product, for error measurement
+ *   orc_attention        causal attention over a KV cache in double:
+ *                        src/cuda_attention.h:28-38 (contract) and the CPU
+ *                        path Transformer::attention, src/model.cpp:217-254
  *
  * Built with -ffp-contract=off so every multiply and add rounds separately,
  * as the reference's C++ source reads.
@@ -30,6 +33,12 @@
  *                reference's matmul_parallel within 1e-5*k (golden fixtures).
  *   rmsnorm      the known values of tests/test_ops.cpp:30-50 and the
  *                reference's rmsnorm (golden fixtures).
+ *   attention    closed forms: a one-position context returns v_0; equal keys
+ *                return the mean of the values; a hand-computed two-position
+ *                answer fixes the 1/sqrt(head_size) scale; constant per-kv-head
+ *                values fix the h / (n_heads / n_kv_heads) head mapping. End to
+ *                end, the forward-pass tests compare logits with the
+ *                reference's compiled Transformer (oracle/_ref/libref_model.so).
  */
 #include <math.h>
 #include <stddef.h>
@@ -155,4 +164,42 @@ size_t orc_argmax(size_t n, const float* x) {
     for (size_t i = 1; i < n; ++i)
         if (x[i] > x[best]) best = i;
     return best;
+}
+
+/* Causal attention, accumulated in double. Row i of q sits at position
+ * pos + i and attends to cache positions [0, pos + i]; query head h reads kv
+ * head h / (n_heads / n_kv_heads); out[i][h*hs + d] =
+ * sum_t softmax_t(q . k_t / sqrt(hs)) v_t[d] (cuda_attention.h:28-38,
+ * model.cpp:217-254). */
+void orc_attention(int n_heads, int n_kv_heads, int hs, size_t rows, size_t pos, const float* q,
+                   size_t q_stride, const float* kc, const float* vc, size_t kv_stride,
+                   double* out, size_t out_stride) {
+    const int group = n_heads / n_kv_heads;
+    double* sc = (double*)malloc((pos + rows) * sizeof(double));
+    for (size_t i = 0; i < rows; ++i) {
+        const size_t n_ctx = pos + i + 1;
+        for (int h = 0; h < n_heads; ++h) {
+            const size_t kv_off = (size_t)(h / group) * (size_t)hs;
+            const float* qh = q + i * q_stride + (size_t)h * (size_t)hs;
+            double mx = -INFINITY;
+            for (size_t t = 0; t < n_ctx; ++t) {
+                double dot = 0.0;
+                for (int d = 0; d < hs; ++d) dot += (double)qh[d] * (double)kc[t * kv_stride + kv_off + d];
+                sc[t] = dot / sqrt((double)hs);
+                if (sc[t] > mx) mx = sc[t];
+            }
+            double sum = 0.0;
+            for (size_t t = 0; t < n_ctx; ++t) {
+                sc[t] = exp(sc[t] - mx);
+                sum += sc[t];
+            }
+            double* oh = out + i * out_stride + (size_t)h * (size_t)hs;
+            for (int d = 0; d < hs; ++d) {
+                double acc = 0.0;
+                for (size_t t = 0; t < n_ctx; ++t) acc += sc[t] * (double)vc[t * kv_stride + kv_off + d];
+                oh[d] = acc / sum;
+            }
+        }
+    }
+    free(sc);
 }

@@ -29,6 +29,81 @@ from tests import inputs  # noqa: E402
 STORIES15M = dict(dim=288, hidden=768, layers=6, heads=6, kv_heads=6, vocab=32000, seq_len=256)
 TINY = dict(dim=16, hidden=40, layers=2, heads=4, kv_heads=2, vocab=29, seq_len=8)
 
+# File order of the per-layer arrays after the embedding (model.cpp:138-149).
+_LAYER_ORDER = ("rms_att", "wq", "wk", "wv", "wo", "rms_ffn", "w1", "w2", "w3")
+
+
+def fixture_model(heads: int, kv_heads: int, shared: bool, seed: int, dim: int = 16,
+                  hidden: int = 40, layers: int = 2, vocab: int = 29, seq_len: int = 8) -> dict:
+    """Raw weights (file layout, projections out x in) drawn as the
+    reference's model-test fixture draws them (checkpoint_fixture.h:30-52):
+    uniform, embedding and classifier in +-1, wq/wk/wv +-0.4, wo/w1/w2/w3
+    +-0.3, rms_att 1 +- 0.2, rms_ffn +-0.2, rms_final +-1. The bits come from
+    tests/inputs.py, not mt19937."""
+    hs = dim // heads
+    kv = kv_heads * hs
+    counter = [seed * 1000]
+
+    def u(shape, scale, offset=0.0):
+        counter[0] += 1
+        return (inputs.uniform(shape, -scale, scale, counter[0]) + np.float32(offset)).astype(
+            np.float32)
+
+    m = dict(dim=dim, hidden=hidden, layers=layers, heads=heads, kv_heads=kv_heads, vocab=vocab,
+             seq_len=seq_len, shared=shared, emb=u((vocab, dim), 1.0))
+    per = {k: [] for k in _LAYER_ORDER}
+    for _ in range(layers):
+        per["rms_att"].append(u((dim,), 0.2, 1.0))
+        per["rms_ffn"].append(u((dim,), 0.2))
+        per["wq"].append(u((dim, dim), 0.4))
+        per["wk"].append(u((kv, dim), 0.4))
+        per["wv"].append(u((kv, dim), 0.4))
+        per["wo"].append(u((dim, dim), 0.3))
+        per["w1"].append(u((hidden, dim), 0.3))
+        per["w2"].append(u((dim, hidden), 0.3))
+        per["w3"].append(u((hidden, dim), 0.3))
+    m.update(per)
+    m["rms_final"] = u((dim,), 1.0)
+    m["wcls"] = None if shared else u((vocab, dim), 1.0)
+    return m
+
+
+def write_raw(path: str, m: dict) -> None:
+    """A llama2.c v0 file from fixture_model()'s arrays."""
+    hs = m["dim"] // m["heads"]
+    header = np.array([m["dim"], m["hidden"], m["layers"], m["heads"], m["kv_heads"],
+                       m["vocab"] if m["shared"] else -m["vocab"], m["seq_len"]], np.int32)
+    parts = [header, m["emb"]]
+    for k in _LAYER_ORDER:
+        parts.extend(m[k])
+    parts.append(m["rms_final"])
+    parts.append(np.full(m["seq_len"] * hs, 123.0, np.float32))
+    if not m["shared"]:
+        parts.append(m["wcls"])
+    with open(path, "wb") as f:
+        for p in parts:
+            f.write(np.ascontiguousarray(p).tobytes())
+
+
+def model_layout(m: dict) -> tuple:
+    """(config, weights) in the CPU model's layout, restating the loader
+    (model.cpp:127-163): projections transposed to in x out, q|k|v and w1|w3
+    concatenated by columns, a tied classifier = the embedding transposed."""
+    cfg = dict(dim=m["dim"], hidden_dim=m["hidden"], n_layers=m["layers"], n_heads=m["heads"],
+               n_kv_heads=m["kv_heads"], vocab_size=m["vocab"], seq_len=m["seq_len"])
+    layers = []
+    for l in range(m["layers"]):
+        layers.append(dict(
+            rms_att=m["rms_att"][l],
+            wqkv=np.concatenate([m["wq"][l].T, m["wk"][l].T, m["wv"][l].T], axis=1),
+            wo=np.ascontiguousarray(m["wo"][l].T),
+            rms_ffn=m["rms_ffn"][l],
+            w13=np.concatenate([m["w1"][l].T, m["w3"][l].T], axis=1),
+            w2=np.ascontiguousarray(m["w2"][l].T)))
+    wcls = m["emb"].T if m["shared"] else m["wcls"].T
+    return cfg, dict(token_embedding=m["emb"], rms_final=m["rms_final"],
+                     wcls=np.ascontiguousarray(wcls, np.float32), layers=layers)
+
 
 def write_checkpoint(path: str, dim: int, hidden: int, layers: int, heads: int, kv_heads: int,
                      vocab: int, seq_len: int, std: float = 0.02, seed: int = 0,

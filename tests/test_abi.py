@@ -91,3 +91,26 @@ def test_skinny_check_precedes_size_check():
     # As in matmul_impl: kernel choice, then the skinny row limit, then 2^31.
     e = err(lambda: em.matmul_f32_raw(9, 1 << 16, 1 << 16, 16, 16, 16, "skinny"))
     assert "at most 8 rows" in str(e)
+
+
+def test_attention_check_rejects_like_the_reference():
+    # test_cuda_attention.cpp:194-210, plus the LDS cap of single_block.
+    em = engine.load()
+    S = em.AttentionShape
+
+    def rejects(shape, kernel):
+        try:
+            em.attention_check(shape, kernel)
+        except em.InvalidArgument:
+            return True
+        return False
+
+    assert rejects(S(2, 2, 6, 64, 36, 12, 12), "split")        # head_size % 4
+    assert not rejects(S(2, 2, 6, 64, 36, 12, 12), "single_block")
+    assert rejects(S(6, 4, 8, 64, 96, 32, 48), "automatic")    # 6 % 4 heads
+    assert rejects(S(4, 4, 8, 0, 64, 32, 32), "automatic")     # seq_len 0
+    assert rejects(S(4, 1, 128, 20000, 768, 128, 512), "single_block")
+    assert not rejects(S(4, 1, 128, 20000, 768, 128, 512), "split")
+    assert rejects(S(4, 4, 8, 64, 64, 32, 32), 7)              # unknown kernel
+    assert em.attention_scratch_floats(S(4, 4, 8, 64, 64, 32, 32), 3, "single_block") == 0
+    assert em.attention_scratch_floats(S(4, 4, 8, 64, 64, 32, 32), 3, "split") > 0

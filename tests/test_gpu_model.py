@@ -1,0 +1,141 @@
+"""The device-resident forward pass (em_model) against the reference's CPU
+Transformer, compiled from its own sources (oracle/_ref/libref_model.so).
+
+Mirrors /root/reference/tests/test_cuda_model.cpp: multi-head with a tied
+classifier, grouped-query with a separate one, multi-query (:119-123), fp32
+and int8 weights; decode over the whole context, prefill in chunks of 1, 1
+and 5 rows, a decode step on that cache and a whole-context prefill that
+rewinds over it (:57-79), every logit within the reference's 1e-4 (:31); and
+the same rejections as the CPU model, after which the cache still works
+(:91-106). Then BASELINE config 4 at the stories15M shape through this
+build's own forward pass: 158-token prefill and 98 greedy decodes, token
+stream identical to the CPU Transformer's.
+"""
+import time
+
+import numpy as np
+import pytest
+
+import oracle
+from tests import e2e_model, engine, inputs
+
+pytestmark = pytest.mark.gpu
+
+em = engine.load()
+lib = oracle.ref_model_lib()
+if lib is None:
+    pytest.skip("oracle/_ref/libref_model.so not built (make -C oracle ref)",
+                allow_module_level=True)
+
+TOL = 1e-4
+
+
+def load(tmp_path, heads, kv_heads, shared):
+    m = e2e_model.fixture_model(heads, kv_heads, shared, seed=heads * 10 + kv_heads)
+    path = str(tmp_path / "model.bin")
+    e2e_model.write_raw(path, m)
+    ck = oracle.RefCheckpoint(lib, path)
+    return ck, ck.weights()
+
+
+def close(gpu, cpu, what):
+    d = float(np.abs(gpu - cpu).max())
+    assert d <= TOL, f"{what}: max diff {d}"
+    return d
+
+
+@pytest.mark.parametrize("wtype", ["f32", "q8"])
+@pytest.mark.parametrize("heads,kv_heads,shared", [(4, 4, True), (4, 2, False), (4, 1, True)],
+                         ids=["mha_tied", "gqa_untied", "mqa_tied"])
+def test_matches_cpu(tmp_path, heads, kv_heads, shared, wtype):
+    ck, w = load(tmp_path, heads, kv_heads, shared)
+    q8 = wtype == "q8"
+    cpu = oracle.RefTransformer(lib, ck, q8)
+    gpu = em.Model(ck.config, w, q8=q8)
+    T, V = ck.config["seq_len"], ck.config["vocab_size"]
+    tokens = [(p * 7 + 3) % V for p in range(T)]
+    worst = 0.0
+    for pos in range(T):
+        print(f"model {heads}/{kv_heads} {wtype} forward pos {pos}", flush=True)
+        worst = max(worst, close(gpu.forward(tokens[pos], pos), cpu.run([tokens[pos]], pos, True),
+                                 f"forward at {pos}"))
+    pos = 0
+    for chunk in (1, 1, 5):
+        part = tokens[pos:pos + chunk]
+        worst = max(worst, close(gpu.forward(part, pos), cpu.run(part, pos), f"prefill at {pos}"))
+        pos += chunk
+    worst = max(worst, close(gpu.forward(tokens[pos], pos), cpu.run([tokens[pos]], pos, True),
+                             "forward after prefill"))
+    worst = max(worst, close(gpu.forward(tokens, 0), cpu.run(tokens, 0), "full prefill"))
+    print(f"{heads}/{kv_heads} {wtype}: worst logit diff {worst:.2e}")
+    gpu.close()
+
+
+def test_bad_inputs_then_cache_still_works(tmp_path):
+    ck, w = load(tmp_path, 4, 2, True)
+    gpu = em.Model(ck.config, w)
+    cpu = oracle.RefTransformer(lib, ck, False)
+    V, T = ck.config["vocab_size"], ck.config["seq_len"]
+    with pytest.raises(em.OutOfRange):
+        gpu.forward(V, 0)
+    with pytest.raises(em.OutOfRange):
+        gpu.forward(-1, 0)
+    with pytest.raises(em.OutOfRange):
+        gpu.forward(0, 1)  # skips position 0
+    with pytest.raises(em.InvalidArgument):
+        gpu.forward(np.array([], np.int32), 0)
+    with pytest.raises(em.OutOfRange):
+        gpu.forward([0] * (T + 1), 0)
+    close(gpu.forward([1, 2, 3], 0), cpu.run([1, 2, 3], 0), "after errors")
+    gpu.close()
+
+
+def test_repeat_gives_identical_bits(tmp_path):
+    # Rewinding and feeding the same tokens again replays the captured graph;
+    # its logits must equal the first pass's bit for bit.
+    ck, w = load(tmp_path, 4, 1, True)
+    gpu = em.Model(ck.config, w, q8=True)
+    T = ck.config["seq_len"]
+    first = [gpu.forward(t % 29, p) for p, t in enumerate(range(3, 3 + T))]
+    second = [gpu.forward(t % 29, p) for p, t in enumerate(range(3, 3 + T))]
+    for a, b in zip(first, second):
+        assert np.array_equal(a, b)
+    gpu.close()
+
+
+@pytest.fixture(scope="module")
+def stories15m(tmp_path_factory):
+    d = tmp_path_factory.mktemp("s15m_model")
+    path = str(d / "model.bin")
+    e2e_model.write_checkpoint(path, seed=15, shared=False, **e2e_model.STORIES15M)
+    ck = oracle.RefCheckpoint(lib, path)
+    prompt = e2e_model.write_prompt(str(d / "prompt.txt"), 158, e2e_model.STORIES15M["vocab"],
+                                    seed=158)
+    return ck, ck.weights(), prompt
+
+
+@pytest.mark.parametrize("wtype", ["f32", "q8"])
+def test_config4_stream_through_device_forward_pass(stories15m, wtype):
+    ck, w, prompt = stories15m
+    q8 = wtype == "q8"
+    cpu = oracle.RefTransformer(lib, ck, q8)
+    gpu = em.Model(ck.config, w, q8=q8)
+    lc, lg = cpu.run(prompt, 0), gpu.forward(prompt, 0)
+    worst = close(lg, lc, "prefill logits")
+    toks_c, toks_g = [int(np.argmax(lc))], [int(np.argmax(lg))]
+    pos = len(prompt)
+    t_gpu = 0.0
+    for step in range(98):
+        lc = cpu.run([toks_c[-1]], pos, True)
+        t0 = time.perf_counter()
+        lg = gpu.forward(toks_g[-1], pos)
+        t_gpu += time.perf_counter() - t0
+        worst = max(worst, float(np.abs(lg - lc).max()))
+        toks_c.append(int(np.argmax(lc)))
+        toks_g.append(int(np.argmax(lg)))
+        pos += 1
+    print(f"config4 {wtype}: worst logit diff {worst:.2e}; gpu decode "
+          f"{t_gpu / 98 * 1e3:.3f} ms/token (host call, graph replay)")
+    assert len(toks_c) == 99
+    assert toks_g == toks_c
+    gpu.close()

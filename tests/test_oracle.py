@@ -275,3 +275,86 @@ def test_live_reference_quant_agrees(orc):
 def test_live_reference_shape_error_names_both_shapes():
     msg = ref.shape_error(2, 3, 4, 2)
     assert "2x3" in msg and "4x2" in msg
+
+
+# ---------------------------------------------------------------- attention
+
+def test_attention_known_answer(orc):
+    # head_size 4: scores 0 and (q . k1) / sqrt(4) = 2 / 2 = 1, so the
+    # weights are 1 / (1 + e) and e / (1 + e) (cuda_attention.h:28-31).
+    q = np.array([[1, 0, 0, 0]], np.float32)
+    kc = np.array([[0, 0, 0, 0], [2, 0, 0, 0]], np.float32)
+    vc = np.array([[1, 0, 0, 0], [0, 1, 0, 0]], np.float32)
+    e = np.e
+    got = orc.attention(1, 1, 4, rows=1, pos=1, q=q, kc=kc, vc=vc)
+    assert np.allclose(got, [[1 / (1 + e), e / (1 + e), 0, 0]], rtol=0, atol=1e-15)
+
+
+def test_attention_one_position_returns_its_value(orc):
+    heads, kv_heads, hs = 4, 2, 8
+    q = inputs.normal((1, heads * hs), 3.0, 301)
+    kc = inputs.normal((5, kv_heads * hs), 3.0, 302)
+    vc = inputs.normal((5, kv_heads * hs), 1.0, 303)
+    got = orc.attention(heads, kv_heads, hs, rows=1, pos=0, q=q, kc=kc, vc=vc)
+    for h in range(heads):
+        kvh = h // (heads // kv_heads)
+        assert np.array_equal(got[0, h * hs:(h + 1) * hs],
+                              vc[0, kvh * hs:(kvh + 1) * hs].astype(np.float64))
+
+
+def test_attention_equal_keys_give_the_mean(orc):
+    hs, n = 16, 7
+    q = inputs.normal((1, hs), 1.0, 311)
+    kc = np.tile(inputs.normal((1, hs), 1.0, 312), (n, 1))
+    vc = inputs.normal((n, hs), 1.0, 313)
+    got = orc.attention(1, 1, hs, rows=1, pos=n - 1, q=q, kc=kc, vc=vc)
+    assert np.allclose(got[0], vc.astype(np.float64).mean(axis=0), rtol=0, atol=1e-12)
+
+
+def test_attention_head_mapping_and_causal_rows(orc):
+    # kv head j holds the constant value j + 1 and zero keys, so query head h
+    # must return h // (heads / kv_heads) + 1; reading kv head h % kv_heads
+    # (a plausible mistake) gives other constants. Row i of a 3-row call at
+    # pos 2 attends to positions [0, 2 + i]: giving position t the value t in
+    # kv head 0 makes the row's output the mean 0..2+i.
+    heads, kv_heads, hs, T = 8, 2, 4, 6
+    vc = np.zeros((T, kv_heads * hs), np.float32)
+    for j in range(kv_heads):
+        vc[:, j * hs:(j + 1) * hs] = j + 1
+    kc = np.zeros_like(vc)
+    q = inputs.normal((1, heads * hs), 1.0, 321)
+    got = orc.attention(heads, kv_heads, hs, rows=1, pos=T - 1, q=q, kc=kc, vc=vc)
+    for h in range(heads):
+        assert np.all(got[0, h * hs:(h + 1) * hs] == h // (heads // kv_heads) + 1)
+    vc2 = np.repeat(np.arange(T, dtype=np.float32)[:, None], kv_heads * hs, axis=1)
+    q3 = inputs.normal((3, heads * hs), 1.0, 322)
+    got = orc.attention(heads, kv_heads, hs, rows=3, pos=2, q=q3, kc=kc, vc=vc2)
+    for i in range(3):
+        assert np.allclose(got[i], np.mean(np.arange(3 + i)), rtol=0, atol=1e-12)
+
+
+# ------------------------------------------------ forward pass: loader layout
+
+needs_ref_model = pytest.mark.skipif(oracle.ref_model_lib() is None,
+                                     reason="oracle/_ref/libref_model.so not built")
+
+
+@needs_ref_model
+@pytest.mark.parametrize("heads,kv_heads,shared", [(4, 4, True), (4, 2, False), (4, 1, True)])
+def test_model_layout_matches_reference_loader(heads, kv_heads, shared, tmp_path):
+    # tests/e2e_model.model_layout restates load_checkpoint's transposes and
+    # concatenations (model.cpp:127-163); the reference's own loader must give
+    # the same arrays bit for bit.
+    from tests import e2e_model
+    m = e2e_model.fixture_model(heads, kv_heads, shared, seed=heads * 10 + kv_heads)
+    path = str(tmp_path / "m.bin")
+    e2e_model.write_raw(path, m)
+    ck = oracle.RefCheckpoint(oracle.ref_model_lib(), path)
+    cfg, w = e2e_model.model_layout(m)
+    assert ck.config == cfg
+    rw = ck.weights()
+    for k in ("token_embedding", "rms_final", "wcls"):
+        assert np.array_equal(rw[k], w[k]), k
+    for l in range(cfg["n_layers"]):
+        for k, v in w["layers"][l].items():
+            assert np.array_equal(rw["layers"][l][k], v), (l, k)
