@@ -65,17 +65,23 @@ def build_library(jobs: int = 0) -> str:
 
 
 def build_cpp_tests() -> str:
-    """The C++ drop-in test (tests/cpp/test_drop_in.cpp), linked against the
-    library and, as its checker, oracle/liboracle.so."""
-    src = os.path.join(ROOT, "tests", "cpp", "test_drop_in.cpp")
-    out = os.path.join(ROOT, "tests", "cpp", "test_drop_in")
-    if not os.path.exists(src):
-        return ""
-    _run(["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", "-I", os.path.join(ROOT, "include"),
-          "-o", out, src, f"-L{HERE}", "-lllm_engine_amd", f"-Wl,-rpath,{HERE}",
-          f"-L{os.path.join(ROOT, 'oracle')}", "-loracle",
-          f"-Wl,-rpath,{os.path.join(ROOT, 'oracle')}", "-lm"])
-    return out
+    """The C++ drop-in tests, linked against the library: tests/cpp/
+    test_drop_in.cpp (checker: oracle/liboracle.so) and
+    tests/cpp/test_cuda_attention.cpp (its own double-precision checker)."""
+    built = []
+    inc = ["-I", os.path.join(ROOT, "include")]
+    link = [f"-L{HERE}", "-lllm_engine_amd", f"-Wl,-rpath,{HERE}"]
+    for name, extra in (("test_drop_in", [f"-L{os.path.join(ROOT, 'oracle')}", "-loracle",
+                                           f"-Wl,-rpath,{os.path.join(ROOT, 'oracle')}"]),
+                        ("test_cuda_attention", [])):
+        src = os.path.join(ROOT, "tests", "cpp", name + ".cpp")
+        out = os.path.join(ROOT, "tests", "cpp", name)
+        if not os.path.exists(src):
+            continue
+        _run(["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", *inc, "-o", out, src, *link,
+              *extra, "-lm"])
+        built.append(out)
+    return " ".join(built)
 
 
 if __name__ == "__main__":
