@@ -44,6 +44,20 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 FP32_MFMA_PEAK_TFLOPS = 157.3
+BF16_MFMA_PEAK_TFLOPS = 2516.6   # MI355X dense bf16 (no sparsity)
+# int8 B at m > 16 runs on bf16 MFMA with A split exactly into three bf16
+# terms: three MFMA products per fp32 multiply-add, so its compute roof in
+# fp32-equivalent flops is a third of the bf16 peak.
+EXACT_SPLIT_PEAK_TFLOPS = BF16_MFMA_PEAK_TFLOPS / 3
+
+
+def q8_kernel(m: int) -> tuple:
+    """(kernel name, compute peak in TFLOP/s) that automatic uses for int8 B."""
+    if m <= 8:
+        return "skinny GEMV (fp32 VALU)", FP32_MFMA_PEAK_TFLOPS / 2
+    if m <= 16:
+        return "tiled_split (fp32 MFMA)", FP32_MFMA_PEAK_TFLOPS
+    return "exact-split bf16 MFMA (3 terms)", EXACT_SPLIT_PEAK_TFLOPS
 METRIC = "int8 GEMV HBM GB/s (m=1, 4096²) + fp32 GEMM TFLOPS (N=4096), % of peak"
 DIM = 4096
 POOL_MIN_BYTES = 600 << 20   # > 512 MiB
@@ -172,14 +186,17 @@ def llama7b_case(em, torch, steps):
         t1, t5 = times1[(k, n)], times512[(k, n)]
         out["decode_m1"][name] = {"us": round(t1, 2),
                                   "GBps": round(gemv_bytes(1, k, n, True) / t1 / 1e3, 1)}
-        out["prefill_m512"][name] = {"us": round(t5, 1),
-                                     "TFLOPS": round(2 * 512 * k * n / t5 / 1e6, 1)}
+        tf = 2 * 512 * k * n / t5 / 1e6
+        out["prefill_m512"][name] = {"us": round(t5, 1), "TFLOPS": round(tf, 1),
+                                     "pct_of_compute_roof": round(100 * tf / q8_kernel(512)[1], 1)}
     out["decode_m1"]["layer_us"] = round(sum(times1[(k, n)] for _, k, n in LLAMA7B_LAYER), 1)
     out["prefill_m512"]["layer_us"] = round(sum(times512[(k, n)] for _, k, n in LLAMA7B_LAYER), 1)
     layer_bytes = sum(gemv_bytes(1, k, n, True) for _, k, n in LLAMA7B_LAYER)
     layer_flops = sum(2 * 512 * k * n for _, k, n in LLAMA7B_LAYER)
     out["decode_m1"]["layer_GBps"] = round(layer_bytes / out["decode_m1"]["layer_us"] / 1e3, 1)
     out["prefill_m512"]["layer_TFLOPS"] = round(layer_flops / out["prefill_m512"]["layer_us"] / 1e6, 1)
+    out["prefill_m512"]["kernel"] = q8_kernel(512)[0]
+    out["prefill_m512"]["compute_roof_TFLOPS"] = round(q8_kernel(512)[1], 1)
     return out
 
 
@@ -362,11 +379,13 @@ def main() -> int:
     if not args.no_extra:
         for m in (4, 16, 64):
             r, _ = gemv_case(em, torch, m, True, max(5, steps // 2), 2)
-            t_mfma = r["flops_per_call"] / (FP32_MFMA_PEAK_TFLOPS * 1e12)
+            kname, peak = q8_kernel(m)
+            t_mfma = r["flops_per_call"] / (peak * 1e12)
             t_hbm = r["bytes_per_call"] / (HBM_PEAK_GBS * 1e9)
             extra[f"int8_gemv_m{m}"] = {"us": round(r["us_per_call"], 3),
                                         "GBps": round(r["GBps"], 1),
                                         "TFLOPS": round(r["flops_per_call"] / r["us_per_call"] / 1e6, 2),
+                                        "kernel": kname, "compute_roof_TFLOPS": round(peak, 1),
                                         "bound": "mfma" if t_mfma > t_hbm else "hbm",
                                         "pct_of_roofline": round(100 * max(t_mfma, t_hbm) * 1e6 / r["us_per_call"], 1)}
         r, _ = gemv_case(em, torch, 1, False, max(5, steps // 2), 2)

@@ -45,12 +45,16 @@ int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, co
                  const float* rms_weight, void* stream) {
     if (kernel < EM_KERNEL_AUTOMATIC || kernel > EM_KERNEL_SKINNY)
         return fail(EM_EINVAL, "matmul_cuda: unknown kernel " + std::to_string(kernel));
-    // automatic: skinny up to 8 rows, as the reference (cuda_matmul.cu:406-410);
-    // above that the B-streaming MFMA kernel at every m it supports (the
-    // reference switches to tiled past 64 rows, but on gfx950 tiled_split
-    // measured as fast or faster up to m = 4096 for int8 B and within 2 %
-    // for fp32), and tiled where B's width or alignment rules it out.
-    if (kernel == EM_KERNEL_AUTOMATIC) kernel = m <= 8 ? EM_KERNEL_SKINNY : EM_KERNEL_TILED_SPLIT;
+    // automatic: skinny up to 8 rows, as the reference (cuda_matmul.cu:406-410).
+    // Above that, the B-streaming fp32 MFMA kernel (tiled_split) at every m
+    // it supports: the reference switches to tiled past 64 rows, but on
+    // gfx950 tiled_split measured as fast or faster up to m = 4096 (within
+    // 2 % for fp32 at 4096^3). From 17 rows, int8 B goes to the exact-split
+    // bf16 MFMA kernel instead (split_bf16.hip: 1.0-2.1x faster from m = 32
+    // to 512 at 4096^2; at m = 16 its extra pass over A loses). tiled takes
+    // what B's width or alignment rules out.
+    const bool automatic = kernel == EM_KERNEL_AUTOMATIC;
+    if (automatic) kernel = m <= 8 ? EM_KERNEL_SKINNY : EM_KERNEL_TILED_SPLIT;
     if (kernel == EM_KERNEL_SKINNY && m > 8)
         return fail(EM_EINVAL,
                     "matmul_cuda: skinny kernel takes at most 8 rows " + shapes(m, n, k));
@@ -82,6 +86,11 @@ int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, co
         a.accumulate = accumulate != 0;
         a.rms_weight = rms_weight;
         a.stream = s;
+        if (std::is_same<BT, int8_t>::value && automatic && m > 16 && split_bf16_supports(a)) {
+            run_split_bf16(a);  // fuses the norm
+            hip_check(hipGetLastError(), "launch");
+            return EM_OK;
+        }
         if (rms_weight && kernel != EM_KERNEL_SKINNY) {
             float* normed = scratch(kNorm, m * k);
             run_rmsnorm_rows(a.m, a.k, A, rms_weight, normed, s);

@@ -100,6 +100,36 @@ __device__ __forceinline__ float ordered_sum(const float* p, size_t stride, int 
     return total;
 }
 
+// Tile of workgroup `id` of a 1-D grid. Workgroups are dispatched to the
+// eight XCDs in turn (id % 8), each XCD with its own L2. With xcd_order the
+// ids are renumbered so that each XCD receives a contiguous run of tiles,
+// row tile fastest: the row tiles that stream the same 256 columns of B run
+// side by side on one XCD and share its L2, instead of landing on eight
+// different L2s. The renumbering is a bijection for any grid size.
+struct TileId {
+    int row, col, slice;
+};
+__device__ __forceinline__ TileId tile_of(int id, int total, int row_tiles, int col_tiles,
+                                          bool xcd_order) {
+    constexpr int kXcds = 8;
+    int idx = id;
+    if (xcd_order) {
+        const int per = total / kXcds, rem = total % kXcds;
+        const int x = id % kXcds, seq = id / kXcds;
+        idx = (x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per) + seq;
+        TileId t;
+        t.row = idx % row_tiles;
+        t.col = (idx / row_tiles) % col_tiles;
+        t.slice = idx / (row_tiles * col_tiles);
+        return t;
+    }
+    TileId t;
+    t.col = idx % col_tiles;
+    t.slice = (idx / col_tiles) % (total / (row_tiles * col_tiles));
+    t.row = idx / (total / row_tiles);
+    return t;
+}
+
 __device__ __forceinline__ floatx4 mfma16x16x4(float a, float b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }

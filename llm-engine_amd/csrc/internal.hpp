@@ -25,8 +25,8 @@ inline void hip_check(hipError_t err, const char* what) {
 // Library-owned, grow-only device scratch (split-K partials, the normed copy
 // of A, quantiser column maxima). Growing waits for the device, frees the old
 // buffer and bumps scratch_generation(). Slot 0 holds partials, slot 1 the
-// norm buffer, slot 2 quantiser work space.
-enum ScratchSlot { kPartial = 0, kNorm = 1, kQuant = 2, kSlots = 3 };
+// norm buffer, slot 2 quantiser work space, slot 3 the bf16 planes of A.
+enum ScratchSlot { kPartial = 0, kNorm = 1, kQuant = 2, kSplitA = 3, kSlots = 4 };
 float* scratch(ScratchSlot slot, std::size_t floats);
 std::size_t scratch_generation();
 
@@ -60,6 +60,12 @@ void run_tiled(const MatmulArgs& a);
 // One thread per element (GpuKernel::naive). A must already be normed.
 template <class BT>
 void run_naive(const MatmulArgs& a);
+
+// int8 B at m > 8 on bf16 MFMA with A split exactly into three bf16 terms
+// (split_bf16.hip). Fuses the norm. Needs n % 16 == 0 and 16-byte aligned B
+// and scales.
+bool split_bf16_supports(const MatmulArgs& a);
+void run_split_bf16(const MatmulArgs& a);
 
 // True if run_tiled_split can take this shape (vector loads of B rows).
 template <class BT>

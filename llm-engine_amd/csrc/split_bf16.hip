@@ -1,0 +1,319 @@
+// int8-weight products on bf16 matrix cores with fp32 results: what
+// GpuKernel::automatic runs for int8 B at m > 16
+// (reference: tiled_split / tiled, /root/reference/src/cuda_matmul.cu:49-125,
+// 350-363; CPU pack_b dequantisation, matmul.cpp:73-90).
+//
+// Exact splitting. Every int8 weight q (|q| <= 127) is exactly a bf16. Every
+// fp32 activation a is exactly hi + mid + lo, three bf16 values: hi keeps a's
+// top 8 significant bits (truncated), mid the next 8 bits of the exact
+// remainder a - hi, lo the last 8 (a 24-bit significand needs no more). So
+// each product hi*q, mid*q, lo*q is exact in fp32 (8 x 8 significant bits),
+// and v_mfma_f32_16x16x32_bf16 sums them into fp32 accumulators. Nothing is
+// dropped: the result differs from an fp32 FMA chain only in summation order,
+// as any reordered fp32 sum does, and the column scale is applied to the
+// finished sum as in the GEMV path. At 16 cycles per 8192 multiply-adds
+// the three terms cost 3/16 of fp32 MFMA time (16x16x4 f32: 32 cycles per
+// 1024); measured against the fp32-MFMA tiled_split kernel at 4096^2 it is
+// 1.2x faster at m = 64 and 2.1x at m = 512, where widening the weights
+// (1.5 VALU ops per byte, once per 16-row block) becomes the next limit.
+//
+//  * split_a_kernel (one pass over A, fused RMSNorm when asked): writes the
+//    three bf16 planes A3[term][m_pad][k_pad], zero-padded to whole tiles, so
+//    the main kernel needs no bounds checks on A.
+//  * split_bf16_kernel<RB>: as tiled_split, B streams from HBM straight into
+//    MFMA operands. A lane (g, j) loads 16 consecutive bytes of 8 rows of a
+//    32-row chunk; MFMA t takes byte t of each, i.e. column 16j + t, as the
+//    8 k-values lane group g supplies (the k order inside the chunk is the
+//    same for A and B). Each byte is widened once and feeds 3 x RB MFMAs
+//    (one per term of A and 16-row block). Chunks ring through two register
+//    sets per wave; the epilogue stages the four waves' sums in LDS and
+//    writes coalesced float4 runs; k slices go through reduce_slices.
+#include <algorithm>
+#include <cstdlib>
+
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace em {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kTile = 256;               // columns per workgroup
+constexpr int kChunk = 32;               // k rows per MFMA step of a wave
+constexpr int kStep = 4 * kChunk;        // the four waves' chunks
+constexpr int kDepth = 2;                // chunks in flight per wave
+constexpr int kTileStride = kTile + 4;   // LDS row stride of the epilogue tile
+
+// --- A -> three bf16 planes -------------------------------------------------
+
+__device__ __forceinline__ uint32_t bits(float f) { return __builtin_bit_cast(uint32_t, f); }
+__device__ __forceinline__ float from_bits(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+// a = hi + mid + lo exactly; each part's bits are the top half of an fp32.
+__device__ __forceinline__ void split3(float a, uint32_t& hi, uint32_t& mid, uint32_t& lo) {
+#pragma clang fp contract(off)
+    hi = bits(a) >> 16;
+    const float r1 = a - from_bits(hi << 16);
+    mid = bits(r1) >> 16;
+    const float r2 = r1 - from_bits(mid << 16);
+    lo = bits(r2) >> 16;
+}
+
+// Row r of A3 (three planes, m_pad x k_pad each): rmsnorm(A[r]) * w when w is
+// given (the arithmetic of rmsnorm_rows: x * s * w[j]), zeros past m and k.
+__global__ __launch_bounds__(kThreads) void split_a_kernel(int m, int k, int m_pad, int k_pad,
+                                                           const float* A, const float* w,
+                                                           uint16_t* A3) {
+    __shared__ float part[4];
+    const int r = blockIdx.x;
+    const float* in = A + static_cast<std::size_t>(r) * k;
+    float s = 1.0f;
+    if (w && r < m) {
+        float ss = 0.0f;
+        for (int j = threadIdx.x; j < k; j += kThreads) ss = fmaf(in[j], in[j], ss);
+        s = 1.0f / sqrtf(block_sum(ss, part) / static_cast<float>(k) + kRmsEps);
+    }
+    const std::size_t plane = static_cast<std::size_t>(m_pad) * k_pad;
+    uint16_t* o = A3 + static_cast<std::size_t>(r) * k_pad;
+    // Eight k per thread per step: one 16-byte store per plane.
+    for (int j0 = threadIdx.x * 8; j0 < k_pad; j0 += kThreads * 8) {
+        uint32_t h[8], md[8], l[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int j = j0 + e;
+            float a = 0.0f;
+            if (r < m && j < k) a = w ? in[j] * s * w[j] : in[j];
+            split3(a, h[e], md[e], l[e]);
+        }
+        auto pack = [](const uint32_t* v) {
+            return make_uint4(v[0] | v[1] << 16, v[2] | v[3] << 16, v[4] | v[5] << 16,
+                              v[6] | v[7] << 16);
+        };
+        *reinterpret_cast<uint4*>(o + j0) = pack(h);
+        *reinterpret_cast<uint4*>(o + plane + j0) = pack(md);
+        *reinterpret_cast<uint4*>(o + 2 * plane + j0) = pack(l);
+    }
+}
+
+// --- the product ---------------------------------------------------------------
+
+struct SbParams {
+    int m, n, k, k_span, m_pad, k_pad;
+    const uint16_t* A3;
+    const int8_t* B;
+    const float* scale;
+    float* out;  // C (direct) or partials [slice][m][n]
+    int accumulate, direct;
+    int row_tiles, col_tiles, xcd_order;
+};
+
+template <int RB>
+struct Chunk {
+    uint4 b[8];         // rows 8g + e of the chunk, 16 columns each
+    uint4 a[RB][3];     // 8 bf16 of each term, row 16 rb + j
+};
+
+// The 8 k-values of column byte t, widened and packed as MFMA's B operand.
+__device__ __forceinline__ bf16x8 column(const uint4 (&b)[8], int t) {
+    const int word = t >> 2, shift = 8 * (t & 3);
+    uint32_t f[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t w = word == 0 ? b[e].x : word == 1 ? b[e].y : word == 2 ? b[e].z : b[e].w;
+        f[e] = bits(static_cast<float>(static_cast<int8_t>(w >> shift)));
+    }
+    uint4 packed;
+    packed.x = __builtin_amdgcn_perm(f[1], f[0], 0x07060302u);
+    packed.y = __builtin_amdgcn_perm(f[3], f[2], 0x07060302u);
+    packed.z = __builtin_amdgcn_perm(f[5], f[4], 0x07060302u);
+    packed.w = __builtin_amdgcn_perm(f[7], f[6], 0x07060302u);
+    return __builtin_bit_cast(bf16x8, packed);
+}
+
+template <int RB>
+__global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
+    __shared__ __attribute__((aligned(16))) float tile[4 * 16 * kTileStride];
+
+    const int tid = threadIdx.x;
+    const int lane = tid % kWave;
+    const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int g = lane >> 4, j = lane & 15;
+    const TileId place = tile_of(blockIdx.x, gridDim.x, p.row_tiles, p.col_tiles,
+                                 p.xcd_order != 0);
+    const int c0 = place.col * kTile;
+    const int m0 = place.row * 16 * RB;
+    const int kb = place.slice * p.k_span;
+    const int ke = min(p.k, kb + p.k_span);
+
+    floatx4 acc[RB][16];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int t = 0; t < 16; ++t) acc[rb][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // A lane whose columns lie past n reads column 0 (its sums are never
+    // stored); rows past k read row k - 1, whose A3 entries are zero. No
+    // load is predicated, so each multiply waits only for its own chunk.
+    const int col = c0 + 16 * j < p.n ? c0 + 16 * j : 0;
+    const std::size_t plane = static_cast<std::size_t>(p.m_pad) * p.k_pad;
+    auto fetch = [&](Chunk<RB>& c, int k0) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const uint16_t* src =
+                p.A3 + static_cast<std::size_t>(m0 + 16 * rb + j) * p.k_pad + k0 + 8 * g;
+#pragma unroll
+            for (int term = 0; term < 3; ++term)
+                c.a[rb][term] = *reinterpret_cast<const uint4*>(src + term * plane);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int r = min(k0 + 8 * g + e, p.k - 1);
+            c.b[e] = stream_load(reinterpret_cast<const uint4*>(
+                p.B + static_cast<uint32_t>(r * p.n + col)));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // Column t + 1 is widened while column t's MFMAs run; the barriers pin
+    // that order (left alone, the scheduler puts each widening right before
+    // its MFMAs, which then wait on it).
+    auto multiply = [&](const Chunk<RB>& c) {
+        bf16x8 bop = column(c.b, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            bf16x8 next = bop;
+            if (t + 1 < 16) next = column(c.b, t + 1);
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                for (int term = 0; term < 3; ++term)
+                    acc[rb][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8, c.a[rb][term]), bop, acc[rb][t], 0, 0, 0);
+            bop = next;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // This wave's chunks: k0 + i * kStep for i < n, in a ring of kDepth
+    // register sets (all in flight before the first multiply); past the last
+    // chunk the ring re-reads it rather than branch around a load.
+    const int k0 = kb + kChunk * w;
+    const int n = k0 < ke ? (ke - k0 + kStep - 1) / kStep : 0;
+    auto at = [&](int i) { return k0 + (i < n ? i : n - 1) * kStep; };
+    if (n > 0) {
+        Chunk<RB> ring[kDepth];
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) fetch(ring[d], at(d));
+        for (int i = 0; i < n; i += kDepth) {
+#pragma unroll
+            for (int d = 0; d < kDepth; ++d) {
+                if (i + d < n) multiply(ring[d]);
+                fetch(ring[d], at(i + d + kDepth));
+            }
+        }
+    }
+
+    // Epilogue, one 16-row block at a time: wave sums into LDS by actual
+    // column, then each thread adds the four waves for 16 consecutive
+    // columns of one row and writes four float4.
+    const int orow = tid / 16, ocol = (tid % 16) * 16;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        if (rb > 0) __syncthreads();
+        float* mine = tile + w * 16 * kTileStride;
+#pragma unroll
+        for (int t = 0; t < 16; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mine[(4 * g + r) * kTileStride + 16 * j + t] = acc[rb][t][r];
+        __syncthreads();
+        const int row = m0 + 16 * rb + orow;
+        if (row < p.m) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int c = c0 + ocol + 4 * q;
+                if (c >= p.n) break;
+                floatx4 v = *reinterpret_cast<const floatx4*>(&tile[orow * kTileStride + ocol + 4 * q]);
+#pragma unroll
+                for (int ww = 1; ww < 4; ++ww)
+                    v += *reinterpret_cast<const floatx4*>(
+                        &tile[(ww * 16 + orow) * kTileStride + ocol + 4 * q]);
+                if (p.direct) {
+                    v *= *reinterpret_cast<const floatx4*>(p.scale + c);
+                    floatx4* o = reinterpret_cast<floatx4*>(p.out + static_cast<std::size_t>(row) * p.n + c);
+                    *o = p.accumulate ? *o + v : v;
+                } else {
+                    *reinterpret_cast<floatx4*>(
+                        p.out + (static_cast<std::size_t>(place.slice) * p.m + row) * p.n + c) = v;
+                }
+            }
+        }
+    }
+}
+
+template <int RB>
+void launch(const SbParams& p, int blocks, hipStream_t s) {
+    hipLaunchKernelGGL((split_bf16_kernel<RB>), dim3(blocks), dim3(kThreads), 0, s, p);
+}
+
+}  // namespace
+
+bool split_bf16_supports(const MatmulArgs& a) {
+    return a.n % 16 == 0 && reinterpret_cast<uintptr_t>(a.B) % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(a.scale) % 16 == 0;
+}
+
+void run_split_bf16(const MatmulArgs& a) {
+    static const int forced_rb = [] {
+        const char* v = std::getenv("EM_SPLIT_ROW_BLOCKS");
+        const int x = v ? std::atoi(v) : 0;
+        return x == 1 || x == 2 || x == 4 ? x : 0;
+    }();
+    // One 16-row block per workgroup keeps the most workgroups in flight and
+    // measured fastest up to m = 256; past that, two blocks per workgroup
+    // halve how often each weight is widened (m = 512: 65 vs 78 us at 4096^2).
+    const int RB = forced_rb ? forced_rb : a.m <= 256 ? 1 : 2;
+    const int row_tiles = ceil_div(a.m, 16 * RB);
+    const int col_tiles = ceil_div(a.n, kTile);
+    const int m_pad = row_tiles * 16 * RB;
+    const int k_pad = ceil_div(a.k, kChunk) * kChunk;
+
+    // A -> A3, with the norm fused.
+    uint16_t* A3 = reinterpret_cast<uint16_t*>(
+        scratch(kSplitA, (static_cast<std::size_t>(3) * m_pad * k_pad + 1) / 2));
+    hipLaunchKernelGGL(split_a_kernel, dim3(m_pad), dim3(kThreads), 0, a.stream, a.m, a.k, m_pad,
+                       k_pad, a.A, a.rms_weight, A3);
+
+    // k slices up to one workgroup per CU, each at least 256 rows deep.
+    const long long blocks = static_cast<long long>(row_tiles) * col_tiles;
+    const int want = static_cast<int>(std::max(1LL, cu_count() / blocks));
+    int slices = std::max(1, std::min(want, ceil_div(a.k, 256)));
+    const int span = ceil_div(ceil_div(a.k, slices), kStep) * kStep;
+    slices = ceil_div(a.k, span);
+
+    SbParams p{};
+    p.m = a.m;
+    p.n = a.n;
+    p.k = a.k;
+    p.k_span = span;
+    p.m_pad = m_pad;
+    p.k_pad = k_pad;
+    p.A3 = A3;
+    p.B = static_cast<const int8_t*>(a.B);
+    p.scale = a.scale;
+    p.direct = slices == 1;
+    p.accumulate = a.accumulate && p.direct;
+    p.out = p.direct ? a.C : scratch(kPartial, static_cast<std::size_t>(slices) * a.m * a.n);
+    p.row_tiles = row_tiles;
+    p.col_tiles = col_tiles;
+    p.xcd_order = 1;
+    const int total = static_cast<int>(blocks) * slices;
+    switch (RB) {
+        case 1: launch<1>(p, total, a.stream); break;
+        case 4: launch<4>(p, total, a.stream); break;
+        default: launch<2>(p, total, a.stream); break;
+    }
+    if (!p.direct) run_reduce_slices(a.m, a.n, slices, p.out, a.scale, a.C, a.accumulate, a.stream);
+}
+
+}  // namespace em

@@ -311,3 +311,44 @@ def test_config3_square_gemm(N):
     if ref is not None:
         want = ref.matmul(A, B, "parallel")
         assert np.abs(got - want).max() <= 1e-5 * N
+
+
+# ------------------------------------------------- exact-split bf16 products
+
+SPLIT_SHAPES = [(17, 300, 32), (24, 4096, 4096), (64, 4096, 4096), (100, 777, 272),
+                (512, 4096, 512), (33, 1029, 256), (64, 31, 48)]
+
+
+@pytest.mark.parametrize("shape", SPLIT_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_exact_split_tighter_than_fp32_tolerance(shape):
+    # automatic sends int8 B at m > 8 to the exact-split bf16 kernel: with A
+    # split exactly into three bf16 terms, its only error is fp32 summation
+    # order, so it must sit far inside the north star's 1e-4 * sum|a||w|.
+    # A spans 1e-20 .. 1e20 within each row, which block-scaled (shared
+    # exponent) formats could not hold; per-element bf16 exponents do.
+    m, k, n = shape
+    mag = np.exp(inputs.uniform((m, k), -46.0, 46.0, 501)).astype(np.float32)
+    sign = np.where(inputs.uniform((m, k), -1.0, 1.0, 502) < 0, -1.0, 1.0).astype(np.float32)
+    A = (mag * sign).astype(np.float32)
+    q, s = orc.quantize_q8(inputs.normal((k, n), 0.02, 503))
+    Bf = orc.dequantize(q, s)
+    exact = orc.matmul_f64(A, Bf)
+    bound = orc.abs_bound(A, Bf)
+    for kernel in ("automatic", "tiled_split"):
+        got = host(em.matmul(dev(A), dev(q), scale=dev(s), kernel=kernel)).astype(np.float64)
+        ratio = float((np.abs(got - exact) / np.maximum(bound, 1e-300)).max())
+        print(f"{shape} {kernel}: max |err| / sum|a||w| = {ratio:.2e}")
+        assert ratio <= 1e-5, (kernel, ratio)
+
+
+def test_exact_split_fused_norm_and_accumulate():
+    m, k, n = 40, 1000, 304
+    A = inputs.normal((m, k), 1.0, 511)
+    w = inputs.uniform((k,), 0.5, 1.5, 512)
+    C0 = inputs.normal((m, n), 1.0, 513)
+    q, s = orc.quantize_q8(inputs.normal((k, n), 0.02, 514))
+    want = orc.matmul_fused(A, Bq=q, scale=s, w=w, C0=C0)
+    C = dev(C0)
+    em.matmul(dev(A), dev(q), C, scale=dev(s), accumulate=True, rms_weight=dev(w))
+    An = orc.rmsnorm(A, w)
+    check(host(C), want, An, orc.dequantize(q, s), k, factor=2.0, C0=C0)
