@@ -157,6 +157,57 @@ LLAMA7B_LAYER = [("wq", 4096, 4096), ("wk", 4096, 4096), ("wv", 4096, 4096), ("w
                  ("w1", 4096, 11008), ("w3", 4096, 11008), ("w2", 11008, 4096)]
 
 
+# The reference's attention benchmark shapes (bench_attention.cpp:93-97):
+# (name, heads, kv_heads, head_size) and its contexts.
+ATTENTION_MODELS = [("stories15M (6 x 48)", 6, 6, 48), ("7B MHA (32 x 128)", 32, 32, 128),
+                    ("8B GQA (32 x 128, 8 kv)", 32, 8, 128)]
+ATTENTION_CONTEXTS = (32, 256, 1024, 4096, 16384)
+
+
+def attention_case(em, torch, reps: int = 20):
+    """Decode attention, one row, per call in a HIP graph, at the last
+    position of each context; K and V rotate over enough copies to exceed
+    512 MiB so they come from HBM. GB/s counts K and V (the reference's
+    bench_attention convention)."""
+    out = {}
+    for name, heads, kv_heads, hs in ATTENTION_MODELS:
+        for n_ctx in ATTENTION_CONTEXTS:
+            if heads == 6 and n_ctx > 256:
+                continue  # stories15M's seq_len is 256
+            dim, kv = heads * hs, kv_heads * hs
+            shape = em.attention_shape(heads, kv_heads, hs, n_ctx, q_stride=dim)
+            kv_bytes = 2 * n_ctx * kv * 4
+            copies = max(1, -(-POOL_MIN_BYTES // kv_bytes))
+            q = torch.randn((1, dim), device="cuda")
+            caches = [(torch.randn((n_ctx, kv), device="cuda"), torch.randn((n_ctx, kv), device="cuda"))
+                      for _ in range(copies)]
+            res = {}
+            for kernel in ("split", "automatic"):
+                scratch = torch.zeros((max(1, em.attention_scratch_floats(shape, 1, kernel)),),
+                                      device="cuda")
+                o = torch.empty((1, dim), device="cuda")
+                pos = torch.full((1,), n_ctx - 1, dtype=torch.int32, device="cuda")
+                stream = torch.cuda.Stream()
+                stream.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(stream):
+                    for kc, vc in caches:
+                        em.attention(shape, 1, pos, q, kc, vc, o, scratch, kernel)
+                torch.cuda.current_stream().wait_stream(stream)
+                torch.cuda.synchronize()
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    for kc, vc in caches:
+                        em.attention(shape, 1, pos, q, kc, vc, o, scratch, kernel)
+                secs, _ = time_graph(torch, g, reps, 2)
+                us = secs / (reps * copies) * 1e6
+                res[kernel] = {"us": round(us, 2), "GBps": round(kv_bytes / us / 1e3, 1)}
+                del g
+            out[f"{name} ctx {n_ctx}"] = res
+            del caches
+            torch.cuda.synchronize()
+    return out
+
+
 def llama7b_case(em, torch, steps):
     """Per-projection and whole-layer times at decode (m = 1, cache-cold
     rotating pools, graph replay) and prefill (m = 512, events over reps)."""
@@ -395,6 +446,7 @@ def main() -> int:
         extra["fp32_gemm_N4096"] = {k: round(v, 3) if isinstance(v, float) else v
                                     for k, v in gemm.items()}
         extra["llama7b_layer_int8"] = llama7b_case(em, torch, steps)
+        extra["decode_attention"] = attention_case(em, torch)
         # The reference's own convention (bench_cuda.cpp:41-54): host time of
         # one launch -> synchronize, median of 101, one W (cache-resident).
         pool = Pool(em, torch, True, DIM, DIM, 1, 99)

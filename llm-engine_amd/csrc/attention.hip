@@ -9,11 +9,14 @@
 //
 // Two kernels, both for 256-thread workgroups of four wave64s:
 //
-//  * split (decode, few rows): workgroup (head group, row, chunk) scores one
+//  * split (decode, few rows): workgroup (head group, row, chunk) covers one
 //    chunk of the context for the G query heads that share a kv head, so a
-//    key or value row is loaded once for all G. A position's key is read by
-//    a power-of-two group of lanes, float4 each, contiguous across the group,
-//    and the dot products are finished with xor shuffles inside the wave.
+//    key or value row is loaded once for all G. A position's key and value
+//    are read by a power-of-two group of lanes, float4 each, contiguous
+//    across the group; every key and value of a 64-position round is loaded
+//    before any is used, and the dot products are finished with xor shuffles
+//    inside the wave. Each lane group keeps an online softmax of its
+//    positions in registers; the groups are merged in LDS in a fixed order.
 //    The chunk's softmax is left unnormalised (max m, sum l, exp-weighted
 //    values o) in scratch, and a second kernel merges the chunks of each
 //    (row, head) in chunk order. The merge is a separate launch rather than a
@@ -65,11 +68,20 @@ std::size_t single_lds(const AttnShape& s) {
     return (static_cast<std::size_t>(s.head_size) + s.seq_len + kThreads) * sizeof(float);
 }
 
+// Lanes per position of the split kernel: head_size / 4 rounded up to a
+// power of two in [4, 64]; F float4 columns per lane.
+int split_lanes(const AttnShape& s) {
+    const int hs4 = s.head_size / 4;
+    int l = 4;
+    while (l < hs4 && l < kWave) l <<= 1;
+    return l;
+}
+int split_f(const AttnShape& s) { return (s.head_size / 4 + split_lanes(s) - 1) / split_lanes(s); }
+
 std::size_t split_lds(const AttnShape& s) {
     const std::size_t G = heads_per_block(s), hs = s.head_size;
-    const std::size_t cap4 = (static_cast<std::size_t>(split_chunk_cap(s)) + 3) / 4 * 4;
-    const std::size_t slots = kThreads / (hs / 4);
-    return (G * hs + G * cap4 + slots * G * hs) * sizeof(float);
+    const std::size_t ns = kThreads / split_lanes(s);
+    return (G * ns * hs + 2 * G * ns) * sizeof(float);
 }
 
 struct SplitScratch {
@@ -110,16 +122,24 @@ __device__ __forceinline__ int lanes_per_row(int n) {
     return l;
 }
 
-template <int G>
-__global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
-    extern __shared__ floatx4 lds4[];
-    __shared__ float2 ml[G];
-    const int hs = a.head_size, hs4 = hs / 4;
-    const int cap4 = (a.chunk_cap + 3) / 4 * 4;
-    floatx4* q_s = lds4;                                    // G x hs4
-    float* sc = reinterpret_cast<float*>(q_s + G * hs4);    // G x cap4
-    floatx4* red = reinterpret_cast<floatx4*>(sc + G * cap4);  // slots x G x hs4
+// Positions a lane group loads per round, at most: all of a round's key and
+// value loads are issued before any is used.
+constexpr int kRoundPerSlot = 8;
 
+// Split workgroup: (head group hg, row i, chunk s). Thread = (slot, sub): the
+// LPP lanes of a slot share a position and hold float4 columns
+// d = sub + f * LPP of it (F per lane). Each slot keeps an online softmax of
+// its positions in registers (running max m, sum l, weighted values o) for
+// the G heads; the NS = 256 / LPP slots are then merged in LDS in slot order.
+template <int G, int LPP, int F>
+__global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
+    constexpr int NS = kThreads / LPP;
+    constexpr int PP = kMinChunk / NS < kRoundPerSlot ? (kMinChunk / NS > 0 ? kMinChunk / NS : 1)
+                                                       : kRoundPerSlot;
+    constexpr int ROUND = NS * PP;
+    extern __shared__ float lds[];
+
+    const int hs = a.head_size, hs4 = hs / 4;
     const int hg = blockIdx.x, i = blockIdx.y, s = blockIdx.z;
     const int n_ctx = *a.pos + i + 1;
     const int chunk = chunk_size(n_ctx, a.splits);
@@ -129,124 +149,190 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
     const int nchunks = (n_ctx + chunk - 1) / chunk;
     const int h0 = hg * G;
     const int kv_off = (h0 / a.group) * hs;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, sub = tid % LPP, slot = tid / LPP;
 
-    // The G heads are adjacent in the row of q.
-    const floatx4* qg = reinterpret_cast<const floatx4*>(
-        a.q + static_cast<std::size_t>(i) * a.q_stride + static_cast<std::size_t>(h0) * hs);
-    for (int j = tid; j < G * hs4; j += kThreads) q_s[j] = qg[j];
-    __syncthreads();
+    // This lane's columns; lanes past hs4 read the last column with a zero
+    // query and store nothing.
+    int dcol[F];
+    bool dok[F];
+#pragma unroll
+    for (int f = 0; f < F; ++f) {
+        const int d = sub + f * LPP;
+        dok[f] = d < hs4;
+        dcol[f] = dok[f] ? d : hs4 - 1;
+    }
+    floatx4 q[G][F];
+    const float* qrow = a.q + static_cast<std::size_t>(i) * a.q_stride + static_cast<std::size_t>(h0) * hs;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int f = 0; f < F; ++f)
+            q[g][f] = dok[f] ? reinterpret_cast<const floatx4*>(qrow + g * hs)[dcol[f]]
+                             : floatx4{0.f, 0.f, 0.f, 0.f};
 
-    // Scores. Every lane runs the same trip count, so the shuffles see whole
-    // waves; lanes past the chunk contribute zeros and store nothing.
-    const int lpp = lanes_per_row(hs4);
-    const int sub = tid % lpp, slot = tid / lpp, nslots = kThreads / lpp;
     const float scale = 1.0f / sqrtf(static_cast<float>(hs));
-    for (int base = 0; base < len; base += nslots) {
-        const int t = base + slot;
-        float dot[G];
+    float m[G], l[G];
+    floatx4 o[G][F];
 #pragma unroll
-        for (int g = 0; g < G; ++g) dot[g] = 0.0f;
-        if (t < len) {
-            const floatx4* k = reinterpret_cast<const floatx4*>(
-                a.kc + static_cast<std::size_t>(t0 + t) * a.kv_stride + kv_off);
-            for (int d = sub; d < hs4; d += lpp) {
-                const floatx4 kv = k[d];
+    for (int g = 0; g < G; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.0f;
 #pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    const floatx4 qv = q_s[g * hs4 + d];
-                    dot[g] += qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
-                }
+        for (int f = 0; f < F; ++f) o[g][f] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    const float* kbase = a.kc + static_cast<std::size_t>(t0) * a.kv_stride + kv_off;
+    const float* vbase = a.vc + static_cast<std::size_t>(t0) * a.kv_stride + kv_off;
+    for (int b0 = 0; b0 < len; b0 += ROUND) {
+        // Every key and value of the round in flight; positions past the
+        // chunk re-read its last position and are masked below.
+        floatx4 kv[PP][F], vv[PP][F];
+#pragma unroll
+        for (int pp = 0; pp < PP; ++pp) {
+            const int t = min(b0 + slot + pp * NS, len - 1);
+            const floatx4* kr = reinterpret_cast<const floatx4*>(kbase + static_cast<std::size_t>(t) * a.kv_stride);
+            const floatx4* vr = reinterpret_cast<const floatx4*>(vbase + static_cast<std::size_t>(t) * a.kv_stride);
+#pragma unroll
+            for (int f = 0; f < F; ++f) {
+                kv[pp][f] = kr[dcol[f]];
+                vv[pp][f] = vr[dcol[f]];
             }
         }
-        for (int o = lpp / 2; o > 0; o >>= 1)
+        float sc[G][PP];
 #pragma unroll
-            for (int g = 0; g < G; ++g) dot[g] += __shfl_xor(dot[g], o, kWave);
-        if (t < len && sub == 0)
+        for (int pp = 0; pp < PP; ++pp) {
+            const bool valid = b0 + slot + pp * NS < len;
 #pragma unroll
-            for (int g = 0; g < G; ++g) sc[g * cap4 + t] = dot[g] * scale;
-    }
-    __syncthreads();
-
-    // The chunk's softmax, unnormalised: one wave per head.
-    const int lane = tid % kWave, wave = tid / kWave;
-    for (int g = wave; g < G; g += kThreads / kWave) {
-        float* row = sc + g * cap4;
-        float m = -INFINITY;
-        for (int t = lane; t < len; t += kWave) m = fmaxf(m, row[t]);
-        m = wave_max(m);
-        float l = 0.0f;
-        for (int t = lane; t < len; t += kWave) {
-            const float e = expf(row[t] - m);
-            row[t] = e;
-            l += e;
-        }
-        l = wave_sum(l);
-        if (lane == 0) ml[g] = make_float2(m, l);
-    }
-    __syncthreads();
-
-    // Weighted values: the hs4 threads of a slot read one value row as
-    // consecutive float4s; slots stride over positions and are added in LDS
-    // in slot order.
-    const int d4 = tid % hs4, r = tid / hs4, slots = kThreads / hs4;
-    if (r < slots) {
-        floatx4 acc[G];
+            for (int g = 0; g < G; ++g) {
+                float dot = 0.0f;
 #pragma unroll
-        for (int g = 0; g < G; ++g) acc[g] = floatx4{0.f, 0.f, 0.f, 0.f};
-        const float* vb = a.vc + static_cast<std::size_t>(t0) * a.kv_stride + kv_off;
-        for (int t = r; t < len; t += slots) {
-            const floatx4 v =
-                reinterpret_cast<const floatx4*>(vb + static_cast<std::size_t>(t) * a.kv_stride)[d4];
+                for (int f = 0; f < F; ++f) {
+                    const floatx4 x = q[g][f] * kv[pp][f];
+                    dot += (x.x + x.y) + (x.z + x.w);
+                }
 #pragma unroll
-            for (int g = 0; g < G; ++g) acc[g] += sc[g * cap4 + t] * v;
+                for (int off = LPP / 2; off > 0; off >>= 1) dot += __shfl_xor(dot, off, kWave);
+                sc[g][pp] = valid ? dot * scale : -INFINITY;
+            }
         }
 #pragma unroll
-        for (int g = 0; g < G; ++g) red[(r * G + g) * hs4 + d4] = acc[g];
+        for (int g = 0; g < G; ++g) {
+            float mb = sc[g][0];
+#pragma unroll
+            for (int pp = 1; pp < PP; ++pp) mb = fmaxf(mb, sc[g][pp]);
+            const float mn = fmaxf(m[g], mb);
+            if (mn == -INFINITY) continue;  // no position of this slot yet
+            const float alpha = expf(m[g] - mn);
+            l[g] *= alpha;
+#pragma unroll
+            for (int f = 0; f < F; ++f) o[g][f] *= alpha;
+#pragma unroll
+            for (int pp = 0; pp < PP; ++pp) {
+                const float e = expf(sc[g][pp] - mn);
+                l[g] += e;
+#pragma unroll
+                for (int f = 0; f < F; ++f) o[g][f] += e * vv[pp][f];
+            }
+            m[g] = mn;
+        }
+    }
+
+    // Merge the slots in slot order: o_s[g][slot][hs], ml_s[g][slot][2].
+    float* o_s = lds;
+    float* ml_s = lds + G * NS * hs;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+        for (int f = 0; f < F; ++f)
+            if (dok[f])
+                reinterpret_cast<floatx4*>(o_s + (g * NS + slot) * hs)[dcol[f]] = o[g][f];
+        if (sub == 0) {
+            ml_s[(g * NS + slot) * 2] = m[g];
+            ml_s[(g * NS + slot) * 2 + 1] = l[g];
+        }
     }
     __syncthreads();
 
     const std::size_t head_row = static_cast<std::size_t>(i) * a.n_heads + h0;
     for (int j = tid; j < G * hs4; j += kThreads) {
         const int g = j / hs4, d = j % hs4;
-        floatx4 o = red[g * hs4 + d];
-        for (int rr = 1; rr < slots; ++rr) o += red[(rr * G + g) * hs4 + d];
+        const float* mlg = ml_s + g * NS * 2;
+        float M = -INFINITY;
+        for (int sl = 0; sl < NS; ++sl) M = fmaxf(M, mlg[2 * sl]);
+        float L = 0.0f;
+        floatx4 O{0.f, 0.f, 0.f, 0.f};
+        for (int sl = 0; sl < NS; ++sl) {
+            const float w = expf(mlg[2 * sl] - M);  // 0 for a slot with no position
+            L += w * mlg[2 * sl + 1];
+            O += w * reinterpret_cast<const floatx4*>(o_s + (g * NS + sl) * hs)[d];
+        }
         if (nchunks == 1) {
-            const float inv = 1.0f / ml[g].y;
             reinterpret_cast<floatx4*>(a.out + static_cast<std::size_t>(i) * a.out_stride +
-                                       static_cast<std::size_t>(h0 + g) * hs)[d] = o * inv;
+                                       static_cast<std::size_t>(h0 + g) * hs)[d] = O * (1.0f / L);
         } else {
-            reinterpret_cast<floatx4*>(a.part_o)[((head_row + g) * a.splits + s) * hs4 + d] = o;
+            reinterpret_cast<floatx4*>(a.part_o)[((head_row + g) * a.splits + s) * hs4 + d] = O;
+            if (d == 0) a.part_ml[(head_row + g) * a.splits + s] = make_float2(M, L);
         }
     }
-    if (nchunks > 1 && tid < G) a.part_ml[(head_row + tid) * a.splits + s] = ml[tid];
 }
 
-// Merges the chunks of one (head, row) in chunk order: m = max m_c,
-// l = sum e^(m_c - m) l_c, out = sum e^(m_c - m) o_c / l.
-__global__ __launch_bounds__(kWave) void attn_merge_kernel(AttnArgs a) {
+// Merges the chunks of one (head, row): m = max m_c,
+// l = sum e^(m_c - m) l_c, out = sum e^(m_c - m) o_c / l. The hs4 threads
+// of a slot take chunks r, r + slots, ... (eight loads in flight), and the
+// slots are added in LDS in slot order, so the result is the same on every
+// call.
+__global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
+    __shared__ float part[4];
+    extern __shared__ floatx4 red4[];  // slots x hs4 values, then slots sums
     const int h = blockIdx.x, i = blockIdx.y;
     const int n_ctx = *a.pos + i + 1;
     const int chunk = chunk_size(n_ctx, a.splits);
     const int n = (n_ctx + chunk - 1) / chunk;
     if (n == 1) return;  // written by the split kernel
     const std::size_t b = (static_cast<std::size_t>(i) * a.n_heads + h) * a.splits;
-    float m = -INFINITY;
-    for (int c = 0; c < n; ++c) m = fmaxf(m, a.part_ml[b + c].x);
+    const int tid = threadIdx.x;
+    float mloc = -INFINITY;
+    for (int c = tid; c < n; c += kThreads) mloc = fmaxf(mloc, a.part_ml[b + c].x);
+    const float M = block_max(mloc, part);
+
     const int hs4 = a.head_size / 4;
+    const int slots = kThreads / hs4, r = tid / hs4, d = tid % hs4;
     const floatx4* po = reinterpret_cast<const floatx4*>(a.part_o);
-    floatx4* out = reinterpret_cast<floatx4*>(a.out + static_cast<std::size_t>(i) * a.out_stride +
-                                              static_cast<std::size_t>(h) * a.head_size);
-    for (int d = threadIdx.x; d < hs4; d += blockDim.x) {
-        float l = 0.0f;
+    float* red_l = reinterpret_cast<float*>(red4 + slots * hs4);
+    if (r < slots) {
         floatx4 acc{0.f, 0.f, 0.f, 0.f};
-        for (int c = 0; c < n; ++c) {
-            const float2 p = a.part_ml[b + c];
-            const float w = expf(p.x - m);
-            l += w * p.y;
-            acc += w * po[(b + c) * hs4 + d];
+        float l = 0.0f;
+        for (int c0 = r; c0 < n; c0 += 8 * slots) {
+            float2 ml[8];
+            floatx4 o[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int c = min(c0 + u * slots, n - 1);
+                ml[u] = a.part_ml[b + c];
+                o[u] = po[(b + c) * hs4 + d];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (c0 + u * slots < n) {
+                    const float w = expf(ml[u].x - M);
+                    l += w * ml[u].y;
+                    acc += w * o[u];
+                }
+            }
         }
-        out[d] = acc * (1.0f / l);
+        red4[r * hs4 + d] = acc;
+        if (d == 0) red_l[r] = l;
+    }
+    __syncthreads();
+    if (tid < hs4) {
+        floatx4 o = red4[tid];
+        float l = red_l[0];
+        for (int rr = 1; rr < slots; ++rr) {
+            o += red4[rr * hs4 + tid];
+            l += red_l[rr];
+        }
+        reinterpret_cast<floatx4*>(a.out + static_cast<std::size_t>(i) * a.out_stride +
+                                   static_cast<std::size_t>(h) * a.head_size)[tid] = o * (1.0f / l);
     }
 }
 
@@ -321,11 +407,25 @@ __global__ __launch_bounds__(kThreads) void attn_single_kernel(AttnArgs a) {
     }
 }
 
-template <int G>
+template <int G, int LPP, int F>
 void launch_split(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t stream) {
     const dim3 grid(s.n_heads / G, rows, a.splits);
-    hipLaunchKernelGGL((attn_split_kernel<G>), grid, dim3(kThreads), split_lds(s), stream, a);
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(s.n_heads, rows), dim3(kWave), 0, stream, a);
+    hipLaunchKernelGGL((attn_split_kernel<G, LPP, F>), grid, dim3(kThreads), split_lds(s), stream, a);
+    const std::size_t hs4 = s.head_size / 4, slots = kThreads / hs4;
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(s.n_heads, rows), dim3(kThreads),
+                       (slots * hs4 * 4 + slots) * sizeof(float), stream, a);
+}
+
+template <int G>
+void launch_split_g(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t stream) {
+    switch (split_lanes(s) * 10 + split_f(s)) {
+        case 41: launch_split<G, 4, 1>(s, a, rows, stream); break;
+        case 81: launch_split<G, 8, 1>(s, a, rows, stream); break;
+        case 161: launch_split<G, 16, 1>(s, a, rows, stream); break;
+        case 321: launch_split<G, 32, 1>(s, a, rows, stream); break;
+        case 641: launch_split<G, 64, 1>(s, a, rows, stream); break;
+        default: launch_split<G, 64, 2>(s, a, rows, stream); break;
+    }
 }
 
 }  // namespace
@@ -340,7 +440,7 @@ std::string attention_reject(const AttnShape& s, int kernel) {
         return "attention: cache past 32-bit indexing";
     const bool single = kernel == kAttnSingle;
     // split loads float4s.
-    if (!single && (s.head_size % 4 || s.head_size > 4 * kThreads || s.q_stride % 4 ||
+    if (!single && (s.head_size % 4 || s.head_size > 512 || s.q_stride % 4 ||
                     s.kv_stride % 4 || s.out_stride % 4))
         return "attention: split needs head_size and strides divisible by 4";
     const std::size_t need = single ? single_lds(s) : split_lds(s);
@@ -388,10 +488,10 @@ void run_attention(const AttnShape& s, int rows, const int* pos, const float* q,
     a.part_o = scratch + l.o;
     a.part_ml = reinterpret_cast<float2*>(scratch + l.ml);
     switch (heads_per_block(s)) {
-        case 8: launch_split<8>(s, a, rows, stream); break;
-        case 4: launch_split<4>(s, a, rows, stream); break;
-        case 2: launch_split<2>(s, a, rows, stream); break;
-        default: launch_split<1>(s, a, rows, stream); break;
+        case 8: launch_split_g<8>(s, a, rows, stream); break;
+        case 4: launch_split_g<4>(s, a, rows, stream); break;
+        case 2: launch_split_g<2>(s, a, rows, stream); break;
+        default: launch_split_g<1>(s, a, rows, stream); break;
     }
 }
 
