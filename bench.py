@@ -208,6 +208,50 @@ def attention_case(em, torch, reps: int = 20):
     return out
 
 
+def llama7b_model_case(em, torch, n_layers: int = 2, n_kv_heads: int = 32, seq_len: int = 1024):
+    """the device-resident forward pass (em_model) at
+    Llama-2-7B dimensions, n_layers deep, int8 weights (random ~N(0, 0.02),
+    drawn on the GPU): a 512-token prefill, then greedy decode steps from
+    position 512, each a host call that returns the logits (graph replay)."""
+    import numpy as np
+    D, H, V, heads = 4096, 11008, 32000, 32
+    KV = n_kv_heads * (D // heads)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(77)
+
+    def rnd(*shape, std=0.02):
+        return (torch.randn(shape, generator=g, device="cuda") * std).cpu().numpy()
+
+    ones = np.ones(D, np.float32)
+    layers = [dict(rms_att=ones, wqkv=rnd(D, D + 2 * KV), wo=rnd(D, D), rms_ffn=ones,
+                   w13=rnd(D, 2 * H), w2=rnd(H, D)) for _ in range(n_layers)]
+    cfg = dict(dim=D, hidden_dim=H, n_layers=n_layers, n_heads=heads, n_kv_heads=n_kv_heads,
+               vocab_size=V, seq_len=seq_len)
+    model = em.Model(cfg, dict(token_embedding=rnd(V, D, std=1.0), rms_final=ones,
+                               wcls=rnd(D, V), layers=layers), q8=True)
+    del layers
+    prompt = [(7 * i + 3) % V for i in range(512)]
+    model.forward(prompt, 0)  # warm-up: grows every buffer
+    t0 = time.perf_counter()
+    reps = 3
+    for _ in range(reps):
+        logits = model.forward(prompt, 0)
+    prefill_s = (time.perf_counter() - t0) / reps
+    tok, pos, steps = int(np.argmax(logits)), 512, 32
+    model.forward(tok, pos)  # eager run + capture
+    t0 = time.perf_counter()
+    for i in range(steps):
+        tok = int(np.argmax(model.forward(tok, pos + 1 + i)))
+    decode_s = (time.perf_counter() - t0) / steps
+    model.close()
+    return {"layers": n_layers, "n_kv_heads": n_kv_heads, "weights": "int8",
+            "prefill_512_ms": round(prefill_s * 1e3, 2),
+            "prefill_tokens_per_s": round(512 / prefill_s, 1),
+            "decode_ms_per_token_at_ctx_512": round(decode_s * 1e3, 3),
+            "note": "host-timed em_model_forward calls (logits downloaded per call); "
+                    "classifier 4096x32000 included"}
+
+
 def llama7b_case(em, torch, steps):
     """Per-projection and whole-layer times at decode (m = 1, cache-cold
     rotating pools, graph replay) and prefill (m = 512, events over reps)."""
@@ -447,6 +491,8 @@ def main() -> int:
                                     for k, v in gemm.items()}
         extra["llama7b_layer_int8"] = llama7b_case(em, torch, steps)
         extra["decode_attention"] = attention_case(em, torch)
+        extra["llama7b_model_2layers_int8"] = llama7b_model_case(em, torch)
+        extra["llama7b_model_2layers_int8_gqa8"] = llama7b_model_case(em, torch, n_kv_heads=8)
         # The reference's own convention (bench_cuda.cpp:41-54): host time of
         # one launch -> synchronize, median of 101, one W (cache-resident).
         pool = Pool(em, torch, True, DIM, DIM, 1, 99)

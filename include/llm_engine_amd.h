@@ -109,7 +109,7 @@ typedef struct {
 } em_attention_shape;
 
 /* Replaces enum class AttentionKernel, cuda_attention.h:15-19. */
-#define EM_ATTN_AUTOMATIC 0    /* split for up to 8 rows, single_block for more */
+#define EM_ATTN_AUTOMATIC 0    /* split for up to 8 rows; more rows: one chunk per row, no merge */
 #define EM_ATTN_SINGLE_BLOCK 1 /* one workgroup per (head, row), scores in LDS */
 #define EM_ATTN_SPLIT 2        /* positions split across workgroups, merged in chunk order */
 

@@ -300,11 +300,12 @@ int em_attention(const em_attention_shape* s, size_t rows, const int* pos_dev, c
         return fail(EM_EINVAL, "attention: more than 2^31 elements");
     if (!pos_dev || !q || !key_cache || !value_cache || !out)
         return fail(EM_EINVAL, "attention: null pointer");
-    const bool split = em::attention_uses_split(sh, rows, kernel);
-    if (split) {
-        if (!scratch) return fail(EM_EINVAL, "attention: split needs scratch");
+    if (em::attention_uses_split(sh, rows, kernel)) {
+        const bool partials = em::attention_needs_scratch(rows, kernel);
+        if (partials && !scratch) return fail(EM_EINVAL, "attention: split needs scratch");
         auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-        if (!a16(q) || !a16(key_cache) || !a16(value_cache) || !a16(out) || !a16(scratch))
+        if (!a16(q) || !a16(key_cache) || !a16(value_cache) || !a16(out) ||
+            (partials && !a16(scratch)))
             return fail(EM_EINVAL, "attention: split needs 16-byte aligned q, caches, out, scratch");
     }
     if (!em::device_present()) return fail(EM_ENODEV, "attention: no usable GPU");

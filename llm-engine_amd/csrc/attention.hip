@@ -24,8 +24,10 @@
 //    measured slower than a second launch, and the fixed merge order keeps
 //    results bit-identical across calls. A context that fits one chunk is
 //    normalised and written by the first kernel; the merge kernel then exits.
-//  * single_block (prefill, many rows): workgroup (head, row) holds the
-//    query and the scores of the whole context in LDS; any head size.
+//    With more than 8 rows (prefill), automatic runs the same kernel with
+//    one chunk per row: the whole context in rounds, no merge.
+//  * single_block (on request): workgroup (head, row) holds the query and
+//    the scores of the whole context in LDS; any head size.
 //
 // The grid is sized for seq_len, never for the position: chunks past the end
 // of a row's context return at once.
@@ -98,9 +100,14 @@ SplitScratch split_scratch(const AttnShape& s, std::size_t rows) {
     return l;
 }
 
-int resolve(const AttnShape& s, int kernel, std::size_t rows) {
+// automatic: the split kernel with chunks across workgroups for up to 8 rows;
+// beyond, rows x heads already fill the GPU, and the same kernel runs one
+// chunk per row (the whole context, in rounds of 64 positions, no merge).
+constexpr int kAttnWhole = 3;
+
+int resolve(int kernel, std::size_t rows) {
     if (kernel != kAttnAutomatic) return kernel;
-    return rows <= kSplitMaxRows || single_lds(s) > kMaxLds ? kAttnSplit : kAttnSingle;
+    return rows <= kSplitMaxRows ? kAttnSplit : kAttnWhole;
 }
 
 struct AttnArgs {
@@ -411,6 +418,7 @@ template <int G, int LPP, int F>
 void launch_split(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t stream) {
     const dim3 grid(s.n_heads / G, rows, a.splits);
     hipLaunchKernelGGL((attn_split_kernel<G, LPP, F>), grid, dim3(kThreads), split_lds(s), stream, a);
+    if (a.splits == 1) return;  // one chunk per row: written directly
     const std::size_t hs4 = s.head_size / 4, slots = kThreads / hs4;
     hipLaunchKernelGGL(attn_merge_kernel, dim3(s.n_heads, rows), dim3(kThreads),
                        (slots * hs4 * 4 + slots) * sizeof(float), stream, a);
@@ -452,18 +460,22 @@ std::string attention_reject(const AttnShape& s, int kernel) {
 
 std::size_t attention_scratch_floats(const AttnShape& s, std::size_t rows, int kernel) {
     if (kernel == kAttnSingle) return 0;
-    if (kernel == kAttnAutomatic && single_lds(s) <= kMaxLds)
-        rows = rows < kSplitMaxRows ? rows : kSplitMaxRows;
+    if (kernel == kAttnAutomatic) rows = rows < kSplitMaxRows ? rows : kSplitMaxRows;
     return split_scratch(s, rows).total;
 }
 
 bool attention_uses_split(const AttnShape& s, std::size_t rows, int kernel) {
-    return resolve(s, kernel, rows) == kAttnSplit;
+    (void)s;
+    return resolve(kernel, rows) != kAttnSingle;
+}
+
+bool attention_needs_scratch(std::size_t rows, int kernel) {
+    return resolve(kernel, rows) == kAttnSplit;
 }
 
 void run_attention(const AttnShape& s, int rows, const int* pos, const float* q, const float* kc,
                    const float* vc, float* out, float* scratch, int kernel, hipStream_t stream) {
-    kernel = resolve(s, kernel, rows);
+    kernel = resolve(kernel, rows);
     AttnArgs a{};
     a.n_heads = s.n_heads;
     a.head_size = s.head_size;
@@ -482,11 +494,16 @@ void run_attention(const AttnShape& s, int rows, const int* pos, const float* q,
                            single_lds(s), stream, a);
         return;
     }
-    const SplitScratch l = split_scratch(s, rows);
-    a.splits = split_count(s.seq_len);
-    a.chunk_cap = split_chunk_cap(s);
-    a.part_o = scratch + l.o;
-    a.part_ml = reinterpret_cast<float2*>(scratch + l.ml);
+    if (kernel == kAttnWhole) {
+        a.splits = 1;
+        a.chunk_cap = s.seq_len;
+    } else {
+        const SplitScratch l = split_scratch(s, rows);
+        a.splits = split_count(s.seq_len);
+        a.chunk_cap = split_chunk_cap(s);
+        a.part_o = scratch + l.o;
+        a.part_ml = reinterpret_cast<float2*>(scratch + l.ml);
+    }
     switch (heads_per_block(s)) {
         case 8: launch_split_g<8>(s, a, rows, stream); break;
         case 4: launch_split_g<4>(s, a, rows, stream); break;

@@ -293,9 +293,28 @@ class RefCheckpoint:
     NAMES = ("token_embedding", "rms_final", "wcls")
     LAYER_NAMES = ("rms_att", "wqkv", "wo", "rms_ffn", "w13", "w2")
 
-    def __init__(self, lib, path: str):
+    def __init__(self, lib, path: Optional[str] = None, config: Optional[dict] = None,
+                 weights: Optional[dict] = None):
+        """From a llama2.c file (the reference's loader), or from `config` and
+        `weights` already in the CPU model's layout."""
         self.lib = lib
-        self.h = lib.ref_ckpt_load(path.encode())
+        if path is not None:
+            self.h = lib.ref_ckpt_load(path.encode())
+        else:
+            keys = ("dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads", "vocab_size",
+                    "seq_len")
+            cfg = (ctypes.c_size_t * 7)(*(int(config[k]) for k in keys))
+            keep = []
+
+            def p(a):
+                a = np.ascontiguousarray(a, np.float32)
+                keep.append(a)
+                return a.ctypes.data
+
+            ptrs = [p(lw[k]) for lw in weights["layers"] for k in self.LAYER_NAMES]
+            arr = (ctypes.c_void_p * len(ptrs))(*ptrs)
+            self.h = lib.ref_ckpt_new(cfg, p(weights["token_embedding"]), arr,
+                                      p(weights["rms_final"]), p(weights["wcls"]))
         if not self.h:
             raise ValueError(lib.ref_model_error().decode())
         cfg = (ctypes.c_size_t * 7)()
@@ -379,6 +398,9 @@ def ref_model_lib():
         lib.ref_ckpt_load.restype = vp
         lib.ref_ckpt_load.argtypes = [ctypes.c_char_p]
         lib.ref_ckpt_free.argtypes = [vp]
+        lib.ref_ckpt_new.restype = vp
+        lib.ref_ckpt_new.argtypes = [ctypes.POINTER(ctypes.c_size_t), vp, ctypes.POINTER(vp), vp,
+                                     vp]
         lib.ref_ckpt_config.argtypes = [vp, ctypes.POINTER(ctypes.c_size_t)]
         lib.ref_ckpt_array.restype = _sz
         lib.ref_ckpt_array.argtypes = [vp, ctypes.c_char_p, _sz, _f32p, _sz]

@@ -9,6 +9,8 @@
 //   ref_ckpt_load / ref_ckpt_config / ref_ckpt_array
 //                         load_checkpoint, Checkpoint, Weights, LayerWeights
 //                         (model.h:11-63, model.cpp:59-163)
+//   ref_ckpt_new          a Checkpoint from arrays already in the CPU model's
+//                         layout (no file), for models too large to write out
 //   ref_model_new / ref_model_run / ref_model_free
 //                         Transformer(ckpt, WeightType), forward / prefill
 //                         (model.h:79-108, model.cpp:194-322)
@@ -61,6 +63,36 @@ void* ref_ckpt_load(const char* path) {
 }
 
 void ref_ckpt_free(void* h) { delete static_cast<Checkpoint*>(h); }
+
+// cfg7: dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len.
+// layers: 6 pointers per layer (rms_att, wqkv, wo, rms_ffn, w13, w2), each
+// array in the layout of struct LayerWeights (model.h:29-36).
+void* ref_ckpt_new(const std::size_t* cfg7, const float* emb, const float* const* layers,
+                   const float* rms_final, const float* wcls) {
+    Checkpoint* c = nullptr;
+    if (guarded([&] {
+            Config cfg{cfg7[0], cfg7[1], cfg7[2], cfg7[3], cfg7[4], cfg7[5], cfg7[6]};
+            const std::size_t D = cfg.dim, H = cfg.hidden_dim, KV = cfg.kv_dim(), V = cfg.vocab_size;
+            auto tensor = [](std::size_t r, std::size_t cols, const float* src) {
+                Tensor t(r, cols);
+                std::memcpy(t.data.data(), src, r * cols * sizeof(float));
+                return t;
+            };
+            auto vec = [](std::size_t n, const float* src) { return std::vector<float>(src, src + n); };
+            c = new Checkpoint{cfg, {}};
+            Weights& w = c->weights;
+            w.token_embedding = tensor(V, D, emb);
+            for (std::size_t l = 0; l < cfg.n_layers; ++l) {
+                const float* const* p = layers + 6 * l;
+                w.layers.push_back({vec(D, p[0]), tensor(D, D + 2 * KV, p[1]), tensor(D, D, p[2]),
+                                    vec(D, p[3]), tensor(D, 2 * H, p[4]), tensor(H, D, p[5])});
+            }
+            w.rms_final = vec(D, rms_final);
+            w.wcls = tensor(D, V, wcls);
+        }))
+        return nullptr;
+    return c;
+}
 
 // dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len.
 void ref_ckpt_config(void* h, std::size_t* out7) {

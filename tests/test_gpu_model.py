@@ -139,3 +139,57 @@ def test_config4_stream_through_device_forward_pass(stories15m, wtype):
     assert len(toks_c) == 99
     assert toks_g == toks_c
     gpu.close()
+
+
+def llama7b_shaped(torch, n_layers, n_kv_heads, seq_len, seed):
+    """Config and CPU-layout weights at Llama-2-7B dimensions (dim 4096,
+    hidden 11008, 32 heads, vocab 32000), n_layers deep: projections and
+    classifier ~N(0, 0.02), embedding ~N(0, 1), RMSNorm gains 1. Drawn on the
+    GPU from a seeded generator (host numpy would take minutes at this size)."""
+    D, H, V, heads = 4096, 11008, 32000, 32
+    KV = n_kv_heads * (D // heads)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+
+    def rnd(*shape, std=0.02):
+        return (torch.randn(shape, generator=g, device="cuda") * std).cpu().numpy()
+
+    layers = [dict(rms_att=np.ones(D, np.float32), wqkv=rnd(D, D + 2 * KV), wo=rnd(D, D),
+                   rms_ffn=np.ones(D, np.float32), w13=rnd(D, 2 * H), w2=rnd(H, D))
+              for _ in range(n_layers)]
+    cfg = dict(dim=D, hidden_dim=H, n_layers=n_layers, n_heads=heads, n_kv_heads=n_kv_heads,
+               vocab_size=V, seq_len=seq_len)
+    w = dict(token_embedding=rnd(V, D, std=1.0), rms_final=np.ones(D, np.float32),
+             wcls=rnd(D, V), layers=layers)
+    return cfg, w
+
+
+@pytest.mark.parametrize("n_kv_heads", [32, 8], ids=["mha", "gqa8"])
+def test_llama7b_shaped_model_matches_cpu(n_kv_heads):
+    # SURVEY 8(f) rank 4: the forward pass at Llama-7B layer shapes (and an
+    # 8-kv-head GQA variant), int8 weights, two layers deep: a 48-token
+    # prefill and 8 greedy decode steps against the reference's CPU
+    # Transformer on the same weights.
+    torch = pytest.importorskip("torch")
+    cfg, w = llama7b_shaped(torch, 2, n_kv_heads, 256, seed=70 + n_kv_heads)
+    ck = oracle.RefCheckpoint(lib, config=cfg, weights=w)
+    cpu = oracle.RefTransformer(lib, ck, True)
+    gpu = em.Model(cfg, w, q8=True)
+    del w
+    prompt = [int(t) for t in inputs._splitmix64(7000 + n_kv_heads, 48) % np.uint64(32000)]
+    lc, lg = cpu.run(prompt, 0), gpu.forward(prompt, 0)
+    scale = float(np.abs(lc).max())
+    worst = float(np.abs(lg - lc).max())
+    toks_c, toks_g = [int(np.argmax(lc))], [int(np.argmax(lg))]
+    pos = len(prompt)
+    for _ in range(8):
+        print(f"llama7b-shaped kv={n_kv_heads} decode pos {pos}", flush=True)
+        lc, lg = cpu.run([toks_c[-1]], pos, True), gpu.forward(toks_g[-1], pos)
+        worst = max(worst, float(np.abs(lg - lc).max()))
+        toks_c.append(int(np.argmax(lc)))
+        toks_g.append(int(np.argmax(lg)))
+        pos += 1
+    print(f"llama7b-shaped kv={n_kv_heads}: worst logit diff {worst:.2e} (max |logit| {scale:.2f})")
+    assert worst <= 1e-4 * max(1.0, scale) * 10, worst
+    assert toks_g == toks_c
+    gpu.close()
