@@ -45,7 +45,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 FP32_MFMA_PEAK_TFLOPS = 157.3
 BF16_MFMA_PEAK_TFLOPS = 2516.6   # MI355X dense bf16 (no sparsity)
-# int8 B at m > 16 runs on bf16 MFMA with A split exactly into three bf16
+# int8 B at m > 8 runs on bf16 MFMA with A split exactly into three bf16
 # terms: three MFMA products per fp32 multiply-add, so its compute roof in
 # fp32-equivalent flops is a third of the bf16 peak.
 EXACT_SPLIT_PEAK_TFLOPS = BF16_MFMA_PEAK_TFLOPS / 3
@@ -55,8 +55,6 @@ def q8_kernel(m: int) -> tuple:
     """(kernel name, compute peak in TFLOP/s) that automatic uses for int8 B."""
     if m <= 8:
         return "skinny GEMV (fp32 VALU)", FP32_MFMA_PEAK_TFLOPS / 2
-    if m <= 16:
-        return "tiled_split (fp32 MFMA)", FP32_MFMA_PEAK_TFLOPS
     return "exact-split bf16 MFMA (3 terms)", EXACT_SPLIT_PEAK_TFLOPS
 METRIC = "int8 GEMV HBM GB/s (m=1, 4096²) + fp32 GEMM TFLOPS (N=4096), % of peak"
 DIM = 4096

@@ -9,6 +9,7 @@
 // a message for em_last_error(); the messages name both shapes as
 // "(A is MxK, B is KxN)", as the reference's exceptions do.
 #include <atomic>
+#include <cstdlib>
 #include <mutex>
 #include <string>
 #include <type_traits>
@@ -49,9 +50,9 @@ int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, co
     // Above that, the B-streaming fp32 MFMA kernel (tiled_split) at every m
     // it supports: the reference switches to tiled past 64 rows, but on
     // gfx950 tiled_split measured as fast or faster up to m = 4096 (within
-    // 2 % for fp32 at 4096^3). From 17 rows, int8 B goes to the exact-split
-    // bf16 MFMA kernel instead (split_bf16.hip: 1.0-2.1x faster from m = 32
-    // to 512 at 4096^2; at m = 16 its extra pass over A loses). tiled takes
+    // 2 % for fp32 at 4096^3). int8 B goes to the exact-split bf16 MFMA
+    // kernel instead (split_bf16.hip: at 4096^2, 1.1x faster than
+    // tiled_split at m = 9-16 and 1.3-2.6x from m = 32 to 512). tiled takes
     // what B's width or alignment rules out.
     const bool automatic = kernel == EM_KERNEL_AUTOMATIC;
     if (automatic) kernel = m <= 8 ? EM_KERNEL_SKINNY : EM_KERNEL_TILED_SPLIT;
@@ -86,7 +87,13 @@ int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, co
         a.accumulate = accumulate != 0;
         a.rms_weight = rms_weight;
         a.stream = s;
-        if (std::is_same<BT, int8_t>::value && automatic && m > 16 && split_bf16_supports(a)) {
+        static const std::size_t split_min_rows = [] {
+            const char* v = std::getenv("EM_SPLIT_MIN_ROWS");  // tuning sweeps
+            const int x = v ? std::atoi(v) : 0;
+            return static_cast<std::size_t>(x > 8 ? x : 9);
+        }();
+        if (std::is_same<BT, int8_t>::value && automatic && m >= split_min_rows &&
+            split_bf16_supports(a)) {
             run_split_bf16(a);  // fuses the norm
             hip_check(hipGetLastError(), "launch");
             return EM_OK;

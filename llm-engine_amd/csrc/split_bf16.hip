@@ -1,5 +1,5 @@
 // int8-weight products on bf16 matrix cores with fp32 results: what
-// GpuKernel::automatic runs for int8 B at m > 16
+// GpuKernel::automatic runs for int8 B at m > 8
 // (reference: tiled_split / tiled, /root/reference/src/cuda_matmul.cu:49-125,
 // 350-363; CPU pack_b dequantisation, matmul.cpp:73-90).
 //
@@ -14,12 +14,14 @@
 // finished sum as in the GEMV path. At 16 cycles per 8192 multiply-adds
 // the three terms cost 3/16 of fp32 MFMA time (16x16x4 f32: 32 cycles per
 // 1024); measured against the fp32-MFMA tiled_split kernel at 4096^2 it is
-// 1.2x faster at m = 64 and 2.1x at m = 512, where widening the weights
-// (1.5 VALU ops per byte, once per 16-row block) becomes the next limit.
+// 1.1x faster at m = 9-16, 1.9x at m = 64 and 2.6x at m = 512, where
+// widening the weights (1.5 VALU ops per byte, once per 16-row block)
+// becomes the next limit.
 //
-//  * split_a_kernel (one pass over A, fused RMSNorm when asked): writes the
-//    three bf16 planes A3[term][m_pad][k_pad], zero-padded to whole tiles, so
-//    the main kernel needs no bounds checks on A.
+//  * split_a_kernel (one pass over A, when RMSNorm is fused or A's rows are
+//    not whole 16-byte groups): writes the three bf16 planes
+//    A3[term][m_pad][k_pad], zero-padded to whole tiles. Otherwise the main
+//    kernel loads fp32 A and splits each 8-value group in registers.
 //  * split_bf16_kernel<RB>: as tiled_split, B streams from HBM straight into
 //    MFMA operands. A lane (g, j) loads 16 consecutive bytes of 8 rows of a
 //    32-row chunk; MFMA t takes byte t of each, i.e. column 16j + t, as the
@@ -100,7 +102,8 @@ __global__ __launch_bounds__(kThreads) void split_a_kernel(int m, int k, int m_p
 
 struct SbParams {
     int m, n, k, k_span, m_pad, k_pad;
-    const uint16_t* A3;
+    const uint16_t* A3;  // the three planes (pre-pass), or
+    const float* A;      // fp32 A, split in registers (RAW kernels)
     const int8_t* B;
     const float* scale;
     float* out;  // C (direct) or partials [slice][m][n]
@@ -108,11 +111,31 @@ struct SbParams {
     int row_tiles, col_tiles, xcd_order;
 };
 
-template <int RB>
+template <int RB, bool RAW>
 struct Chunk {
     uint4 b[8];         // rows 8g + e of the chunk, 16 columns each
     uint4 a[RB][3];     // 8 bf16 of each term, row 16 rb + j
 };
+
+// RAW: the 8 fp32 values of row 16 rb + j as loaded; split in multiply().
+template <int RB>
+struct Chunk<RB, true> {
+    uint4 b[8];
+    floatx4 a[RB][2];
+    bool aok;           // false past k: the A values count as zero
+};
+
+// Eight fp32 values -> the three bf16 terms, packed as MFMA A operands.
+__device__ __forceinline__ void split8(const floatx4& x0, const floatx4& x1, uint4 (&t)[3]) {
+    uint32_t h[8], md[8], l[8];
+    const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) split3(v[e], h[e], md[e], l[e]);
+    t[0] = make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16);
+    t[1] = make_uint4(md[0] | md[1] << 16, md[2] | md[3] << 16, md[4] | md[5] << 16,
+                      md[6] | md[7] << 16);
+    t[2] = make_uint4(l[0] | l[1] << 16, l[2] | l[3] << 16, l[4] | l[5] << 16, l[6] | l[7] << 16);
+}
 
 // The 8 k-values of column byte t, widened and packed as MFMA's B operand.
 __device__ __forceinline__ bf16x8 column(const uint4 (&b)[8], int t) {
@@ -131,7 +154,7 @@ __device__ __forceinline__ bf16x8 column(const uint4 (&b)[8], int t) {
     return __builtin_bit_cast(bf16x8, packed);
 }
 
-template <int RB>
+template <int RB, bool RAW>
 __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
     __shared__ __attribute__((aligned(16))) float tile[4 * 16 * kTileStride];
 
@@ -157,14 +180,31 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
     // load is predicated, so each multiply waits only for its own chunk.
     const int col = c0 + 16 * j < p.n ? c0 + 16 * j : 0;
     const std::size_t plane = static_cast<std::size_t>(p.m_pad) * p.k_pad;
-    auto fetch = [&](Chunk<RB>& c, int k0) {
+    auto fetch = [&](Chunk<RB, RAW>& c, int k0) {
+        if constexpr (RAW) {
+            // k % 8 == 0, so a lane's 8 values are all inside k or all past
+            // it; past k (and past m) it reads valid memory and is masked or
+            // never stored.
+            const int kk = k0 + 8 * g;
+            c.aok = kk < p.k;
+            const int kl = c.aok ? kk : p.k - 8;
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-            const uint16_t* src =
-                p.A3 + static_cast<std::size_t>(m0 + 16 * rb + j) * p.k_pad + k0 + 8 * g;
+            for (int rb = 0; rb < RB; ++rb) {
+                const int row = min(m0 + 16 * rb + j, p.m - 1);
+                const floatx4* src =
+                    reinterpret_cast<const floatx4*>(p.A + static_cast<std::size_t>(row) * p.k + kl);
+                c.a[rb][0] = src[0];
+                c.a[rb][1] = src[1];
+            }
+        } else {
 #pragma unroll
-            for (int term = 0; term < 3; ++term)
-                c.a[rb][term] = *reinterpret_cast<const uint4*>(src + term * plane);
+            for (int rb = 0; rb < RB; ++rb) {
+                const uint16_t* src =
+                    p.A3 + static_cast<std::size_t>(m0 + 16 * rb + j) * p.k_pad + k0 + 8 * g;
+#pragma unroll
+                for (int term = 0; term < 3; ++term)
+                    c.a[rb][term] = *reinterpret_cast<const uint4*>(src + term * plane);
+            }
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -177,7 +217,18 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
     // Column t + 1 is widened while column t's MFMAs run; the barriers pin
     // that order (left alone, the scheduler puts each widening right before
     // its MFMAs, which then wait on it).
-    auto multiply = [&](const Chunk<RB>& c) {
+    auto multiply = [&](const Chunk<RB, RAW>& c) {
+        uint4 aop[RB][3];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            if constexpr (RAW) {
+                const floatx4 z{0.f, 0.f, 0.f, 0.f};
+                split8(c.aok ? c.a[rb][0] : z, c.aok ? c.a[rb][1] : z, aop[rb]);
+            } else {
+#pragma unroll
+                for (int term = 0; term < 3; ++term) aop[rb][term] = c.a[rb][term];
+            }
+        }
         bf16x8 bop = column(c.b, 0);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -189,7 +240,7 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
 #pragma unroll
                 for (int term = 0; term < 3; ++term)
                     acc[rb][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        __builtin_bit_cast(bf16x8, c.a[rb][term]), bop, acc[rb][t], 0, 0, 0);
+                        __builtin_bit_cast(bf16x8, aop[rb][term]), bop, acc[rb][t], 0, 0, 0);
             bop = next;
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -202,7 +253,7 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
     const int n = k0 < ke ? (ke - k0 + kStep - 1) / kStep : 0;
     auto at = [&](int i) { return k0 + (i < n ? i : n - 1) * kStep; };
     if (n > 0) {
-        Chunk<RB> ring[kDepth];
+        Chunk<RB, RAW> ring[kDepth];
 #pragma unroll
         for (int d = 0; d < kDepth; ++d) fetch(ring[d], at(d));
         for (int i = 0; i < n; i += kDepth) {
@@ -252,8 +303,12 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
 }
 
 template <int RB>
-void launch(const SbParams& p, int blocks, hipStream_t s) {
-    hipLaunchKernelGGL((split_bf16_kernel<RB>), dim3(blocks), dim3(kThreads), 0, s, p);
+void launch(const SbParams& p, int blocks, bool raw, hipStream_t s) {
+    if (raw) {
+        hipLaunchKernelGGL((split_bf16_kernel<RB, true>), dim3(blocks), dim3(kThreads), 0, s, p);
+    } else {
+        hipLaunchKernelGGL((split_bf16_kernel<RB, false>), dim3(blocks), dim3(kThreads), 0, s, p);
+    }
 }
 
 }  // namespace
@@ -278,11 +333,17 @@ void run_split_bf16(const MatmulArgs& a) {
     const int m_pad = row_tiles * 16 * RB;
     const int k_pad = ceil_div(a.k, kChunk) * kChunk;
 
-    // A -> A3, with the norm fused.
-    uint16_t* A3 = reinterpret_cast<uint16_t*>(
-        scratch(kSplitA, (static_cast<std::size_t>(3) * m_pad * k_pad + 1) / 2));
-    hipLaunchKernelGGL(split_a_kernel, dim3(m_pad), dim3(kThreads), 0, a.stream, a.m, a.k, m_pad,
-                       k_pad, a.A, a.rms_weight, A3);
+    // Without a norm, the kernel splits A itself, chunk by chunk (needs whole
+    // 8-value groups and 16-byte rows); otherwise a pre-pass writes the three
+    // planes with the norm fused.
+    const bool raw = !a.rms_weight && a.k % 8 == 0 && reinterpret_cast<uintptr_t>(a.A) % 16 == 0;
+    uint16_t* A3 = nullptr;
+    if (!raw) {
+        A3 = reinterpret_cast<uint16_t*>(
+            scratch(kSplitA, (static_cast<std::size_t>(3) * m_pad * k_pad + 1) / 2));
+        hipLaunchKernelGGL(split_a_kernel, dim3(m_pad), dim3(kThreads), 0, a.stream, a.m, a.k,
+                           m_pad, k_pad, a.A, a.rms_weight, A3);
+    }
 
     // k slices up to one workgroup per CU, each at least 256 rows deep.
     const long long blocks = static_cast<long long>(row_tiles) * col_tiles;
@@ -299,6 +360,7 @@ void run_split_bf16(const MatmulArgs& a) {
     p.m_pad = m_pad;
     p.k_pad = k_pad;
     p.A3 = A3;
+    p.A = a.A;
     p.B = static_cast<const int8_t*>(a.B);
     p.scale = a.scale;
     p.direct = slices == 1;
@@ -309,9 +371,9 @@ void run_split_bf16(const MatmulArgs& a) {
     p.xcd_order = 1;
     const int total = static_cast<int>(blocks) * slices;
     switch (RB) {
-        case 1: launch<1>(p, total, a.stream); break;
-        case 4: launch<4>(p, total, a.stream); break;
-        default: launch<2>(p, total, a.stream); break;
+        case 1: launch<1>(p, total, raw, a.stream); break;
+        case 4: launch<4>(p, total, raw, a.stream); break;
+        default: launch<2>(p, total, raw, a.stream); break;
     }
     if (!p.direct) run_reduce_slices(a.m, a.n, slices, p.out, a.scale, a.C, a.accumulate, a.stream);
 }

@@ -315,7 +315,7 @@ def test_config3_square_gemm(N):
 
 # ------------------------------------------------- exact-split bf16 products
 
-SPLIT_SHAPES = [(17, 300, 32), (24, 4096, 4096), (64, 4096, 4096), (100, 777, 272),
+SPLIT_SHAPES = [(9, 300, 32), (12, 4096, 4096), (24, 4096, 4096), (64, 4096, 4096), (100, 777, 272),
                 (512, 4096, 512), (33, 1029, 256), (64, 31, 48)]
 
 
