@@ -250,6 +250,43 @@ def llama7b_model_case(em, torch, n_layers: int = 2, n_kv_heads: int = 32, seq_l
                     "classifier 4096x32000 included"}
 
 
+def stories15m_case(em, torch, steps: int = 98):
+    """BASELINE config 4's shape through the device-resident forward pass:
+    stories15M (dim 288, 6 layers, 6 heads, hidden 768, vocab 32000, seq 256),
+    random weights ~N(0, 0.02), a 158-token prefill then `steps` greedy
+    decodes; host-timed em_model_forward calls (logits downloaded per call)."""
+    import numpy as np
+    D, H, L, V, S = 288, 768, 6, 32000, 256
+    g = torch.Generator(device="cuda")
+    g.manual_seed(15)
+
+    def rnd(*shape):
+        return (torch.randn(shape, generator=g, device="cuda") * 0.02).cpu().numpy()
+
+    ones = np.ones(D, np.float32)
+    cfg = dict(dim=D, hidden_dim=H, n_layers=L, n_heads=6, n_kv_heads=6, vocab_size=V, seq_len=S)
+    w = dict(token_embedding=rnd(V, D), rms_final=ones, wcls=rnd(D, V),
+             layers=[dict(rms_att=ones, wqkv=rnd(D, 3 * D), wo=rnd(D, D), rms_ffn=ones,
+                          w13=rnd(D, 2 * H), w2=rnd(H, D)) for _ in range(L)])
+    prompt = [(11 * i + 5) % V for i in range(158)]
+    out = {}
+    for wtype in ("f32", "q8"):
+        model = em.Model(cfg, w, q8=wtype == "q8")
+        for rep in range(2):  # the first pass grows buffers and captures the graph
+            t0 = time.perf_counter()
+            logits = model.forward(prompt, 0)
+            prefill_s = time.perf_counter() - t0
+            tok = int(np.argmax(logits))
+            t0 = time.perf_counter()
+            for i in range(steps):  # positions 158 .. 158 + steps - 1
+                tok = int(np.argmax(model.forward(tok, 158 + i)))
+            decode_s = (time.perf_counter() - t0) / steps
+        out[wtype] = {"prefill_158_ms": round(prefill_s * 1e3, 3),
+                      "decode_ms_per_token": round(decode_s * 1e3, 4)}
+        model.close()
+    return out
+
+
 def llama7b_case(em, torch, steps):
     """Per-projection and whole-layer times at decode (m = 1, cache-cold
     rotating pools, graph replay) and prefill (m = 512, events over reps)."""
@@ -489,6 +526,7 @@ def main() -> int:
                                     for k, v in gemm.items()}
         extra["llama7b_layer_int8"] = llama7b_case(em, torch, steps)
         extra["decode_attention"] = attention_case(em, torch)
+        extra["stories15m_forward"] = stories15m_case(em, torch)
         extra["llama7b_model_2layers_int8"] = llama7b_model_case(em, torch)
         extra["llama7b_model_2layers_int8_gqa8"] = llama7b_model_case(em, torch, n_kv_heads=8)
         # The reference's own convention (bench_cuda.cpp:41-54): host time of

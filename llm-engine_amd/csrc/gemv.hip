@@ -231,8 +231,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
 
 // Deepest rows-per-lane that fits the register file without spilling: with
 // 16 int8 columns per lane, more than one row of A holds 32+ accumulators
-// and 16 loads in flight would pass 256 VGPRs.
-constexpr int max_depth(int E, int MM) { return (E == 16 && MM > 1) ? 8 : 16; }
+// and 16 loads in flight would pass 256 VGPRs. One row of A leaves room for
+// 32 loads in flight (128 VGPRs).
+constexpr int max_depth(int E, int MM) { return MM == 1 ? 32 : (E == 16 ? 8 : 16); }
 
 template <class BT, int MM, int E, int L, bool NORM>
 void launch(const GemvParams<BT>& p, dim3 grid, hipStream_t s) {
@@ -260,6 +261,7 @@ void pick_depth(int L, const GemvParams<BT>& p, dim3 grid, hipStream_t s) {
         switch (L) {
             case 4: pick_rows<BT, E, 4, NORM>(p, grid, s); break;
             case 8: pick_rows<BT, E, 8, NORM>(p, grid, s); break;
+            case 32: pick_rows<BT, E, 32, NORM>(p, grid, s); break;
             default: pick_rows<BT, E, 16, NORM>(p, grid, s); break;
         }
     }
@@ -278,8 +280,9 @@ bool aligned(const void* ptr, size_t bytes) {
     return reinterpret_cast<uintptr_t>(ptr) % bytes == 0;
 }
 
-// Rows per lane: the deepest of 16 / 8 / 4 that still gives the grid half a
-// workgroup per CU or more. Deep slices mean fewer partials to reduce; with
+// Rows per lane: if all of k fits one slice and n is wide, the shallowest
+// depth that holds it. Otherwise the deepest of 16 / 8 / 4 that still gives the grid
+// half a workgroup per CU or more. Deep slices mean fewer partials to reduce; with
 // nontemporal weight loads one 16-row-deep workgroup per CU streams a
 // 4096^2 int8 matrix faster than two 8-deep ones, and sweeps over the
 // Llama-7B and stories15M shapes put the cut near CUs / 2.
@@ -295,8 +298,14 @@ int rows_per_lane(int E, int m, int n, int k) {
     const int mm = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
     const int cap = max_depth(E, mm);
     int L = 4;
-    if (forced == 4 || forced == 8 || forced == 16) {
+    if (forced == 4 || forced == 8 || forced == 16 || forced == 32) {
         L = forced;
+    } else if (k <= E * cap && ceil_div(n, kThreads) >= cu_count() / 4) {
+        // All of k in one slice when the columns alone give a quarter of a
+        // workgroup per CU: no partials and no second launch (the stories15M
+        // classifier, k = 288, n = 32000). Narrower products still split k,
+        // since a handful of workgroups cannot keep enough loads in flight.
+        while (E * L < k) L *= 2;
     } else {
         const long long tiles = ceil_div(n, kThreads);
         const long long target = cu_count() / 2;
