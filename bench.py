@@ -207,7 +207,7 @@ def attention_case(em, torch, reps: int = 20):
 
 
 def llama7b_model_case(em, torch, n_layers: int = 2, n_kv_heads: int = 32, seq_len: int = 1024):
-    """the device-resident forward pass (em_model) at
+    """The device-resident forward pass (em_model) at
     Llama-2-7B dimensions, n_layers deep, int8 weights (random ~N(0, 0.02),
     drawn on the GPU): a 512-token prefill, then greedy decode steps from
     position 512, each a host call that returns the logits (graph replay)."""
@@ -393,6 +393,32 @@ def profile_pass(em, torch, sweeps: int = 2) -> dict:
             "bytes_per_product": gemv_bytes(1, DIM, DIM, True)}
 
 
+def profile_gemm_pass(em, torch, N: int = 4096, reps: int = 5) -> dict:
+    """Eager fp32 GEMMs (`tiled`, N^3, the metric's second half) for rocprofv3
+    counter passes over the MFMA kernel: `reps` launches after 2 warm-ups."""
+    A = torch.rand((N, N), device="cuda") * 2 - 1
+    B = torch.rand((N, N), device="cuda") * 2 - 1
+    C = torch.empty((N, N), device="cuda")
+    for _ in range(2 + reps):
+        em.matmul(A, B, C, kernel="tiled")
+    torch.cuda.synchronize()
+    return {"gemm_N": N, "launches": 2 + reps, "flops_per_launch": 2 * N**3}
+
+
+def profile_split_pass(em, torch, m: int = 512, reps: int = 20) -> dict:
+    """Eager int8 products at m rows over the rotating 4096^2 pool with the
+    `automatic` kernel (exact-split bf16 above 8 rows), for counter passes."""
+    per_copy = DIM * DIM
+    copies = -(-POOL_MIN_BYTES // per_copy)
+    pool = Pool(em, torch, True, DIM, DIM, copies, 1000)
+    A = torch.randn((m, DIM), device="cuda")
+    C = torch.empty((m, DIM), device="cuda")
+    for i in range(reps):
+        em.matmul(A, pool.ws[i % copies], C, scale=pool.scales[i % copies])
+    torch.cuda.synchronize()
+    return {"m": m, "launches": reps, "flops_per_launch": 2 * m * DIM * DIM}
+
+
 def measured_traffic():
     """HBM bytes per headline call from the committed counter summary, or None."""
     path = os.path.join(ROOT, "profiles", "gemv_int8_m1_4096_traffic.json")
@@ -448,14 +474,16 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
-    ap.add_argument("--profile-pass", action="store_true",
-                    help="eager launches for rocprofv3 --pmc (calibration copy + headline)")
+    ap.add_argument("--profile-pass", nargs="?", const="gemv", choices=["gemv", "gemm", "split"],
+                    help="eager launches for rocprofv3 --pmc: gemv (calibration copy + "
+                         "headline, the default), gemm (fp32 tiled N=4096) or split "
+                         "(int8 m=512, exact-split)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: every box in this run has one GPU, and the matmul "
-              "path has no multi-GPU code (it would shard W by output columns, one slab per GPU; "
-              "see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "path has no multi-GPU code (it would shard W by output columns, one slab per "
+              "GPU). Run with --gpus 1.", file=sys.stderr)
         return 2
 
     import torch
@@ -463,6 +491,12 @@ def main() -> int:
     if not torch.cuda.is_available() or not em.available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
+    if args.profile_pass == "gemm":
+        print(json.dumps(profile_gemm_pass(em, torch)))
+        return 0
+    if args.profile_pass == "split":
+        print(json.dumps(profile_split_pass(em, torch)))
+        return 0
     if args.profile_pass:
         print(json.dumps(profile_pass(em, torch)))
         return 0

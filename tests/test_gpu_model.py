@@ -166,7 +166,7 @@ def llama7b_shaped(torch, n_layers, n_kv_heads, seq_len, seed):
 
 @pytest.mark.parametrize("n_kv_heads", [32, 8], ids=["mha", "gqa8"])
 def test_llama7b_shaped_model_matches_cpu(n_kv_heads):
-    # the forward pass at Llama-7B layer shapes (and an
+    # The forward pass at Llama-7B layer shapes (and an
     # 8-kv-head GQA variant), int8 weights, two layers deep: a 48-token
     # prefill and 8 greedy decode steps against the reference's CPU
     # Transformer on the same weights.
