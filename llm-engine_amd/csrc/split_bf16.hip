@@ -14,9 +14,11 @@
 // finished sum as in the GEMV path. At 16 cycles per 8192 multiply-adds
 // the three terms cost 3/16 of fp32 MFMA time (16x16x4 f32: 32 cycles per
 // 1024); measured against the fp32-MFMA tiled_split kernel at 4096^2 it is
-// 1.1x faster at m = 9-16, 1.9x at m = 64 and 2.6x at m = 512, where
-// widening the weights (1.5 VALU ops per byte, once per 16-row block)
-// becomes the next limit.
+// 1.1x faster at m = 9-16, 1.9x at m = 64 and 2.6x at m = 512. VALU work
+// does not overlap the MFMA pipe on gfx950 (each VALU op beside a bf16 MFMA
+// adds ~1.4 ns to it), so the kernel's speed is set by VALU ops per MFMA:
+// widening the weights (1.5 per byte, once per row tile) and splitting A
+// (5.5 per value, once per column tile).
 //
 //  * split_a_kernel (one pass over A, when RMSNorm is fused or A's rows are
 //    not whole 16-byte groups): writes the three bf16 planes
@@ -125,16 +127,27 @@ struct Chunk<RB, true> {
     bool aok;           // false past k: the A values count as zero
 };
 
-// Eight fp32 values -> the three bf16 terms, packed as MFMA A operands.
+// Eight fp32 values -> the three bf16 terms, packed as MFMA A operands: the
+// split3 arithmetic, with each term's top halves paired by one byte permute
+// (4.5 VALU ops per value; the MFMA pipe does not hide VALU work, so this
+// count sets the kernel's speed as much as the MFMAs do).
 __device__ __forceinline__ void split8(const floatx4& x0, const floatx4& x1, uint4 (&t)[3]) {
-    uint32_t h[8], md[8], l[8];
+#pragma clang fp contract(off)
     const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    uint32_t a[8], r1[8], r2[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) split3(v[e], h[e], md[e], l[e]);
-    t[0] = make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16);
-    t[1] = make_uint4(md[0] | md[1] << 16, md[2] | md[3] << 16, md[4] | md[5] << 16,
-                      md[6] | md[7] << 16);
-    t[2] = make_uint4(l[0] | l[1] << 16, l[2] | l[3] << 16, l[4] | l[5] << 16, l[6] | l[7] << 16);
+    for (int e = 0; e < 8; ++e) {
+        a[e] = bits(v[e]);
+        const float f1 = v[e] - from_bits(a[e] & 0xffff0000u);
+        r1[e] = bits(f1);
+        r2[e] = bits(f1 - from_bits(r1[e] & 0xffff0000u));
+    }
+    auto pair = [](const uint32_t* x, int e) {
+        return __builtin_amdgcn_perm(x[e + 1], x[e], 0x07060302u);  // top halves, x[e] low
+    };
+    t[0] = make_uint4(pair(a, 0), pair(a, 2), pair(a, 4), pair(a, 6));
+    t[1] = make_uint4(pair(r1, 0), pair(r1, 2), pair(r1, 4), pair(r1, 6));
+    t[2] = make_uint4(pair(r2, 0), pair(r2, 2), pair(r2, 4), pair(r2, 6));
 }
 
 // The 8 k-values of column byte t, widened and packed as MFMA's B operand.
@@ -154,7 +167,10 @@ __device__ __forceinline__ bf16x8 column(const uint4 (&b)[8], int t) {
     return __builtin_bit_cast(bf16x8, packed);
 }
 
-template <int RB, bool RAW>
+// RAW: A arrives as fp32 and is split in registers (else as the three planes
+// of split_a_kernel). WHOLE: k is a multiple of the chunk, so every chunk
+// lies inside k and no row or value needs a clamp or a mask.
+template <int RB, bool RAW, bool WHOLE>
 __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
     __shared__ __attribute__((aligned(16))) float tile[4 * 16 * kTileStride];
 
@@ -180,37 +196,51 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
     // load is predicated, so each multiply waits only for its own chunk.
     const int col = c0 + 16 * j < p.n ? c0 + 16 * j : 0;
     const std::size_t plane = static_cast<std::size_t>(p.m_pad) * p.k_pad;
+    // This lane's rows of A (rows past m read row m - 1; their sums are
+    // never stored), from which each chunk is one offset away.
+    const float* a_row[RB];
+    const uint16_t* a3_row[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        if constexpr (RAW) {
+            a_row[rb] = p.A + static_cast<std::size_t>(min(m0 + 16 * rb + j, p.m - 1)) * p.k + 8 * g;
+        } else {
+            a3_row[rb] = p.A3 + static_cast<std::size_t>(m0 + 16 * rb + j) * p.k_pad + 8 * g;
+        }
+    }
+    const int8_t* b_lane = p.B + static_cast<uint32_t>(8 * g * p.n + col);
     auto fetch = [&](Chunk<RB, RAW>& c, int k0) {
         if constexpr (RAW) {
             // k % 8 == 0, so a lane's 8 values are all inside k or all past
-            // it; past k (and past m) it reads valid memory and is masked or
-            // never stored.
-            const int kk = k0 + 8 * g;
-            c.aok = kk < p.k;
-            const int kl = c.aok ? kk : p.k - 8;
+            // it; past k it reads valid memory and is masked.
+            int kl = k0;
+            if constexpr (!WHOLE) {
+                c.aok = k0 + 8 * g < p.k;
+                kl = c.aok ? k0 : p.k - 8 - 8 * g;
+            }
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
-                const int row = min(m0 + 16 * rb + j, p.m - 1);
-                const floatx4* src =
-                    reinterpret_cast<const floatx4*>(p.A + static_cast<std::size_t>(row) * p.k + kl);
+                const floatx4* src = reinterpret_cast<const floatx4*>(a_row[rb] + kl);
                 c.a[rb][0] = src[0];
                 c.a[rb][1] = src[1];
             }
         } else {
 #pragma unroll
-            for (int rb = 0; rb < RB; ++rb) {
-                const uint16_t* src =
-                    p.A3 + static_cast<std::size_t>(m0 + 16 * rb + j) * p.k_pad + k0 + 8 * g;
+            for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
                 for (int term = 0; term < 3; ++term)
-                    c.a[rb][term] = *reinterpret_cast<const uint4*>(src + term * plane);
-            }
+                    c.a[rb][term] = *reinterpret_cast<const uint4*>(a3_row[rb] + k0 + term * plane);
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int r = min(k0 + 8 * g + e, p.k - 1);
-            c.b[e] = stream_load(reinterpret_cast<const uint4*>(
-                p.B + static_cast<uint32_t>(r * p.n + col)));
+            if constexpr (WHOLE) {
+                c.b[e] = stream_load(reinterpret_cast<const uint4*>(
+                    b_lane + static_cast<uint32_t>((k0 + e) * p.n)));
+            } else {
+                const int r = min(k0 + 8 * g + e, p.k - 1);
+                c.b[e] = stream_load(reinterpret_cast<const uint4*>(
+                    p.B + static_cast<uint32_t>(r * p.n + col)));
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -221,9 +251,11 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
         uint4 aop[RB][3];
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
-            if constexpr (RAW) {
+            if constexpr (RAW && !WHOLE) {
                 const floatx4 z{0.f, 0.f, 0.f, 0.f};
                 split8(c.aok ? c.a[rb][0] : z, c.aok ? c.a[rb][1] : z, aop[rb]);
+            } else if constexpr (RAW) {
+                split8(c.a[rb][0], c.a[rb][1], aop[rb]);
             } else {
 #pragma unroll
                 for (int term = 0; term < 3; ++term) aop[rb][term] = c.a[rb][term];
@@ -304,10 +336,15 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
 
 template <int RB>
 void launch(const SbParams& p, int blocks, bool raw, hipStream_t s) {
-    if (raw) {
-        hipLaunchKernelGGL((split_bf16_kernel<RB, true>), dim3(blocks), dim3(kThreads), 0, s, p);
+    const bool whole = p.k % kChunk == 0;
+    if (raw && whole) {
+        hipLaunchKernelGGL((split_bf16_kernel<RB, true, true>), dim3(blocks), dim3(kThreads), 0, s, p);
+    } else if (raw) {
+        hipLaunchKernelGGL((split_bf16_kernel<RB, true, false>), dim3(blocks), dim3(kThreads), 0, s, p);
+    } else if (whole) {
+        hipLaunchKernelGGL((split_bf16_kernel<RB, false, true>), dim3(blocks), dim3(kThreads), 0, s, p);
     } else {
-        hipLaunchKernelGGL((split_bf16_kernel<RB, false>), dim3(blocks), dim3(kThreads), 0, s, p);
+        hipLaunchKernelGGL((split_bf16_kernel<RB, false, false>), dim3(blocks), dim3(kThreads), 0, s, p);
     }
 }
 
@@ -325,9 +362,10 @@ void run_split_bf16(const MatmulArgs& a) {
         return x == 1 || x == 2 || x == 4 ? x : 0;
     }();
     // One 16-row block per workgroup keeps the most workgroups in flight and
-    // measured fastest up to m = 256; past that, two blocks per workgroup
-    // halve how often each weight is widened (m = 512: 65 vs 78 us at 4096^2).
-    const int RB = forced_rb ? forced_rb : a.m <= 256 ? 1 : 2;
+    // measured fastest up to m = 256; past that, more blocks per workgroup
+    // cut how often each weight is widened (4096^2: two blocks at m = 512,
+    // 49 vs 61 us for one; four from m = 1024, 90 vs 95 us for two).
+    const int RB = forced_rb ? forced_rb : a.m <= 256 ? 1 : a.m < 1024 ? 2 : 4;
     const int row_tiles = ceil_div(a.m, 16 * RB);
     const int col_tiles = ceil_div(a.n, kTile);
     const int m_pad = row_tiles * 16 * RB;
