@@ -315,8 +315,12 @@ def test_config3_square_gemm(N):
 
 # ------------------------------------------------- exact-split bf16 products
 
+# Covers one, two and four 16-row blocks per workgroup (m <= 256, < 1024,
+# >= 1024), k whole chunks of 32 or ragged, k not a multiple of 8 (pre-split
+# planes), and m and n that end inside a tile.
 SPLIT_SHAPES = [(9, 300, 32), (12, 4096, 4096), (24, 4096, 4096), (64, 4096, 4096), (100, 777, 272),
-                (512, 4096, 512), (33, 1029, 256), (64, 31, 48)]
+                (512, 4096, 512), (33, 1029, 256), (64, 31, 48), (300, 4096, 256), (1024, 1024, 512),
+                (1040, 520, 272), (1100, 301, 160)]
 
 
 @pytest.mark.parametrize("shape", SPLIT_SHAPES, ids=lambda s: "x".join(map(str, s)))
