@@ -93,6 +93,14 @@ def lib() -> ctypes.CDLL:
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise ImportError(f"{LIB_PATH} is not built: run python llm-engine_amd/build.py")
+        # PyTorch ships its own HIP runtime under the same soname
+        # (libamdhip64.so.7). Loaded first, it is the one this library binds
+        # to, so one process has one runtime; loaded after this library
+        # brought in /opt/rocm's, torch finds no device.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = ctypes.CDLL(LIB_PATH)
         L.em_last_error.restype = ctypes.c_char_p
         L.em_available.restype = ctypes.c_int

@@ -46,9 +46,18 @@ def _run(cmd):
     return r
 
 
+# Per-file additions. attention.hip: the tile kernel rescales its MFMA
+# accumulators with VALU ops after every key block; in the default AGPR form
+# each rescale copies them out of and back into AGPRs (~300 moves per 128
+# MFMAs), so its MFMAs write VGPRs instead.
+FILE_FLAGS = {
+    "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    _run([HIPCC, *HIP_FLAGS, "-c", src, "-o", obj])
+    _run([HIPCC, *HIP_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj])
     return obj
 
 

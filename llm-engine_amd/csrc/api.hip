@@ -308,7 +308,7 @@ int em_attention(const em_attention_shape* s, size_t rows, const int* pos_dev, c
     if (!pos_dev || !q || !key_cache || !value_cache || !out)
         return fail(EM_EINVAL, "attention: null pointer");
     if (em::attention_uses_split(sh, rows, kernel)) {
-        const bool partials = em::attention_needs_scratch(rows, kernel);
+        const bool partials = em::attention_needs_scratch(sh, rows, kernel);
         if (partials && !scratch) return fail(EM_EINVAL, "attention: split needs scratch");
         auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
         if (!a16(q) || !a16(key_cache) || !a16(value_cache) || !a16(out) ||

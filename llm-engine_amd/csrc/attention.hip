@@ -100,18 +100,28 @@ SplitScratch split_scratch(const AttnShape& s, std::size_t rows) {
     return l;
 }
 
-// automatic: the split kernel with chunks across workgroups for up to 8 rows;
-// beyond, rows x heads already fill the GPU, and the same kernel runs one
-// chunk per row (the whole context, in rounds of 64 positions, no merge).
+// automatic: the split kernel with chunks across workgroups for up to 8 rows.
+// Beyond, the tile kernel (16 query rows per wave on fp32 MFMA, each key and
+// value row loaded once per 16 rows) for head sizes it is built for; other
+// head sizes run the split kernel with one chunk per row (the whole context,
+// in rounds of 64 positions, no merge).
 constexpr int kAttnWhole = 3;
+constexpr int kAttnTile = 4;
+constexpr int kTileRows = 16;        // query rows per tile wave
+constexpr int kTileMaxHeadSize = 128;
 
-int resolve(int kernel, std::size_t rows) {
+bool tile_supports(const AttnShape& s) {
+    return s.head_size % 16 == 0 && s.head_size <= kTileMaxHeadSize;
+}
+
+int resolve(int kernel, std::size_t rows, const AttnShape& s) {
     if (kernel != kAttnAutomatic) return kernel;
-    return rows <= kSplitMaxRows ? kAttnSplit : kAttnWhole;
+    if (rows <= kSplitMaxRows) return kAttnSplit;
+    return tile_supports(s) ? kAttnTile : kAttnWhole;
 }
 
 struct AttnArgs {
-    int n_heads, head_size, group, seq_len, splits, chunk_cap;
+    int n_heads, head_size, group, seq_len, splits, chunk_cap, rows;
     int q_stride, kv_stride, out_stride;
     const int* pos;
     const float* q;
@@ -414,6 +424,177 @@ __global__ __launch_bounds__(kThreads) void attn_single_kernel(AttnArgs a) {
     }
 }
 
+// --- prefill rows: tiles of 16 queries on fp32 MFMA ------------------------
+//
+// One wave per (query head, 16 consecutive rows). For each block of 16
+// cached positions it forms S^T = K Q^T (positions x queries) with
+// v_mfma_f32_16x16x4_f32, then O^T += V^T P^T. In lane l (g = l / 16,
+// j = l % 16):
+//  * S^T: the lane supplies K[position j][d] and Q[query j][d] for the head
+//    dims d of its lane group's quarter (4E contiguous floats, E = hs / 16),
+//    so its key and query loads are float4 runs; both operands take the
+//    head dims in the same order.
+//  * S^T's output layout leaves in the lane the scores of query j at
+//    positions 4g + r (r = 0..3) of the block: exactly the B operand
+//    P^T[position 4g + r][query j] of k-step r of the V product, so scores
+//    never leave the lane's registers.
+//  * V^T: lane j supplies rows d = E j + c (c = 0..E-1, one MFMA each), E
+//    contiguous floats of a value row; output block c then holds
+//    O[query j][E (4g + r) + c], so the lane ends with 4E contiguous head
+//    dims of its query.
+//  * Every accumulator of a lane belongs to query j: the online softmax
+//    rescale is one factor per lane. The block max takes two xor shuffles
+//    (the four lane groups of a query); the sum is combined once, at the end.
+// Positions past a query's own are masked, and blocks past the wave's last
+// row are never read; the next block's keys and values are loaded while
+// this one is used (two register sets, alternating; a 32-position block
+// measured no faster and needs twice the registers).
+template <int E>
+struct TileBlock {
+    floatx4 k[E];   // K[t0 + j][4E g .. 4E g + 4E)
+    float v[4][E];  // per r: V[t0 + 4g + r][E j .. E j + E)
+};
+
+template <int E>
+__device__ __forceinline__ void load_run(const float* src, float* dst) {
+    if constexpr (E % 4 == 0) {
+#pragma unroll
+        for (int u = 0; u < E / 4; ++u) {
+            const floatx4 x = reinterpret_cast<const floatx4*>(src)[u];
+            dst[4 * u] = x.x;
+            dst[4 * u + 1] = x.y;
+            dst[4 * u + 2] = x.z;
+            dst[4 * u + 3] = x.w;
+        }
+    } else if constexpr (E % 2 == 0) {
+#pragma unroll
+        for (int u = 0; u < E / 2; ++u) {
+            const float2 x = reinterpret_cast<const float2*>(src)[u];
+            dst[2 * u] = x.x;
+            dst[2 * u + 1] = x.y;
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < E; ++u) dst[u] = src[u];
+    }
+}
+
+template <int E>
+__global__ __launch_bounds__(kWave) void attn_tile_kernel(AttnArgs a) {
+    constexpr int HS = 16 * E, Q4 = 4 * E;
+    constexpr int KB = 16;  // positions per block
+    const int lane = threadIdx.x, g = lane >> 4, j = lane & 15;
+    const int h = blockIdx.x, r0 = blockIdx.y * kTileRows;
+    const int pos0 = *a.pos;
+    const int row = min(r0 + j, a.rows - 1);  // rows past the call: computed, not stored
+    const int pq = pos0 + row;                // this lane's query position
+    const int last = pos0 + min(r0 + kTileRows - 1, a.rows - 1);  // the wave's last position
+    const float* kbase = a.kc + static_cast<std::size_t>((h / a.group) * HS);
+    const float* vbase = a.vc + static_cast<std::size_t>((h / a.group) * HS);
+
+    float q[Q4];
+    load_run<Q4>(a.q + static_cast<std::size_t>(row) * a.q_stride + static_cast<std::size_t>(h) * HS + Q4 * g, q);
+
+    // Positions past `last` re-read position `last` (in the cache: the
+    // caller keeps *pos + rows <= seq_len) and are masked.
+    auto load = [&](TileBlock<E>& b, int t0) {
+        const int tk = min(t0 + j, last);
+        const floatx4* kr = reinterpret_cast<const floatx4*>(
+            kbase + static_cast<std::size_t>(tk) * a.kv_stride + Q4 * g);
+#pragma unroll
+        for (int u = 0; u < E; ++u) b.k[u] = kr[u];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tv = min(t0 + 4 * g + r, last);
+            load_run<E>(vbase + static_cast<std::size_t>(tv) * a.kv_stride + E * j, b.v[r]);
+        }
+    };
+
+    const float scale = 1.0f / sqrtf(static_cast<float>(HS));
+    float m = -INFINITY, l = 0.0f;
+    floatx4 o[E];
+#pragma unroll
+    for (int c = 0; c < E; ++c) o[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    auto use = [&](const TileBlock<E>& b, int t0) {
+        // S^T in four accumulators (head-dim steps u mod 4), so consecutive
+        // MFMAs are independent, added pairwise at the end.
+        floatx4 sacc[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) sacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < Q4; ++u) sacc[u & 3] = mfma16x16x4(b.k[u / 4][u % 4], q[u], sacc[u & 3]);
+        float sv[4];
+        float mb = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = t0 + 4 * g + r;
+            const float x = ((sacc[0][r] + sacc[1][r]) + (sacc[2][r] + sacc[3][r])) * scale;
+            sv[r] = t <= pq ? x : -INFINITY;
+            mb = fmaxf(mb, sv[r]);
+        }
+        mb = fmaxf(mb, __shfl_xor(mb, 16, kWave));
+        mb = fmaxf(mb, __shfl_xor(mb, 32, kWave));
+        // Position 0 is in every query's context, so mn is finite from the
+        // first block on; before it, m = -inf gives alpha = 0.
+        const float mn = fmaxf(m, mb);
+        const float alpha = expf(m - mn);
+        l *= alpha;
+#pragma unroll
+        for (int c = 0; c < E; ++c) o[c] *= alpha;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float p = expf(sv[r] - mn);
+            l += p;
+#pragma unroll
+            for (int c = 0; c < E; ++c) o[c] = mfma16x16x4(b.v[r][c], p, o[c]);
+        }
+        m = mn;
+    };
+
+    TileBlock<E> b0, b1;
+    load(b0, 0);
+    for (int t0 = 0; t0 <= last; t0 += 2 * KB) {
+        if (t0 + KB <= last) load(b1, t0 + KB);
+        use(b0, t0);
+        if (t0 + KB > last) break;
+        if (t0 + 2 * KB <= last) load(b0, t0 + 2 * KB);
+        use(b1, t0 + KB);
+    }
+
+    // The four lane groups of query j hold partial sums of its denominator;
+    // the xor pairs add them in the same order in every lane.
+    l += __shfl_xor(l, 16, kWave);
+    l += __shfl_xor(l, 32, kWave);
+    if (r0 + j < a.rows) {
+        const float inv = 1.0f / l;
+        floatx4* dst = reinterpret_cast<floatx4*>(a.out + static_cast<std::size_t>(r0 + j) * a.out_stride +
+                                                  static_cast<std::size_t>(h) * HS + Q4 * g);
+        float run[Q4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int c = 0; c < E; ++c) run[E * r + c] = o[c][r] * inv;
+#pragma unroll
+        for (int u = 0; u < E; ++u)
+            dst[u] = floatx4{run[4 * u], run[4 * u + 1], run[4 * u + 2], run[4 * u + 3]};
+    }
+}
+
+void launch_tile(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t stream) {
+    const dim3 grid(s.n_heads, (rows + kTileRows - 1) / kTileRows);
+    switch (s.head_size / 16) {
+        case 1: hipLaunchKernelGGL(attn_tile_kernel<1>, grid, dim3(kWave), 0, stream, a); break;
+        case 2: hipLaunchKernelGGL(attn_tile_kernel<2>, grid, dim3(kWave), 0, stream, a); break;
+        case 3: hipLaunchKernelGGL(attn_tile_kernel<3>, grid, dim3(kWave), 0, stream, a); break;
+        case 4: hipLaunchKernelGGL(attn_tile_kernel<4>, grid, dim3(kWave), 0, stream, a); break;
+        case 5: hipLaunchKernelGGL(attn_tile_kernel<5>, grid, dim3(kWave), 0, stream, a); break;
+        case 6: hipLaunchKernelGGL(attn_tile_kernel<6>, grid, dim3(kWave), 0, stream, a); break;
+        case 7: hipLaunchKernelGGL(attn_tile_kernel<7>, grid, dim3(kWave), 0, stream, a); break;
+        default: hipLaunchKernelGGL(attn_tile_kernel<8>, grid, dim3(kWave), 0, stream, a); break;
+    }
+}
+
 template <int G, int LPP, int F>
 void launch_split(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t stream) {
     const dim3 grid(s.n_heads / G, rows, a.splits);
@@ -465,17 +646,16 @@ std::size_t attention_scratch_floats(const AttnShape& s, std::size_t rows, int k
 }
 
 bool attention_uses_split(const AttnShape& s, std::size_t rows, int kernel) {
-    (void)s;
-    return resolve(kernel, rows) != kAttnSingle;
+    return resolve(kernel, rows, s) != kAttnSingle;
 }
 
-bool attention_needs_scratch(std::size_t rows, int kernel) {
-    return resolve(kernel, rows) == kAttnSplit;
+bool attention_needs_scratch(const AttnShape& s, std::size_t rows, int kernel) {
+    return resolve(kernel, rows, s) == kAttnSplit;
 }
 
 void run_attention(const AttnShape& s, int rows, const int* pos, const float* q, const float* kc,
                    const float* vc, float* out, float* scratch, int kernel, hipStream_t stream) {
-    kernel = resolve(kernel, rows);
+    kernel = resolve(kernel, rows, s);
     AttnArgs a{};
     a.n_heads = s.n_heads;
     a.head_size = s.head_size;
@@ -489,6 +669,11 @@ void run_attention(const AttnShape& s, int rows, const int* pos, const float* q,
     a.kc = kc;
     a.vc = vc;
     a.out = out;
+    a.rows = rows;
+    if (kernel == kAttnTile) {
+        launch_tile(s, a, rows, stream);
+        return;
+    }
     if (kernel == kAttnSingle) {
         hipLaunchKernelGGL(attn_single_kernel, dim3(s.n_heads, rows), dim3(kThreads),
                            single_lds(s), stream, a);

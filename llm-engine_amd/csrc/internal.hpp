@@ -104,10 +104,10 @@ enum AttnKernel { kAttnAutomatic = 0, kAttnSingle = 1, kAttnSplit = 2 };
 // "" if `kernel` can run shape `s`, else the reason.
 std::string attention_reject(const AttnShape& s, int kernel);
 std::size_t attention_scratch_floats(const AttnShape& s, std::size_t rows, int kernel);
-// True if the call runs the float4 split kernel (16-byte alignment needed);
-// attention_needs_scratch: true if it also writes per-chunk partials.
+// True if the call runs a float4 kernel, split or tile (16-byte alignment
+// needed); attention_needs_scratch: true if it also writes per-chunk partials.
 bool attention_uses_split(const AttnShape& s, std::size_t rows, int kernel);
-bool attention_needs_scratch(std::size_t rows, int kernel);
+bool attention_needs_scratch(const AttnShape& s, std::size_t rows, int kernel);
 // Rows [0, rows) at positions *pos + i; the caller guarantees *pos + rows <= seq_len.
 void run_attention(const AttnShape& s, int rows, const int* pos, const float* q, const float* kc,
                    const float* vc, float* out, float* scratch, int kernel, hipStream_t stream);

@@ -68,6 +68,27 @@ def test_kernels_match_double_reference(case, kernel):
     print(f"{case} {kernel}: worst {worst:.2e}")
 
 
+# Prefill rows (automatic, more than 8): the tile kernel for head sizes that
+# are multiples of 16 up to 128 (every register layout it is built for, MHA,
+# GQA, MQA), the one-chunk-per-row split kernel for the rest (20, 144).
+PREFILL_CASES = [(4, 4, 16, 200), (8, 2, 64, 700), (4, 1, 80, 300), (2, 1, 96, 300),
+                 (3, 3, 112, 200), (8, 2, 128, 700), (6, 6, 48, 256), (4, 4, 32, 300),
+                 (4, 2, 20, 200), (2, 2, 144, 300)]
+
+
+@pytest.mark.parametrize("case", PREFILL_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_prefill_rows_match_double_reference(case):
+    # Row counts that fill 16-row tiles exactly and leave them ragged;
+    # starting positions on and across 16-position block edges, and the end
+    # of the cache.
+    T = case[3]
+    worst = 0.0
+    for i, rows in enumerate((9, 16, 17, 40, 100)):
+        worst = max(worst, run_case(case, "automatic", (0, 15, 16, 31, 33, T - rows),
+                                    rows, seed=7400 + 10 * i))
+    print(f"{case} prefill: worst {worst:.2e}")
+
+
 def test_long_context_split_and_automatic():
     # Past single_block's LDS cap (test_cuda_attention.cpp:174-192).
     case = (4, 1, 128, 20000)
