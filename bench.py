@@ -206,11 +206,9 @@ def attention_case(em, torch, reps: int = 20):
     return out
 
 
-def llama7b_model_case(em, torch, n_layers: int = 2, n_kv_heads: int = 32, seq_len: int = 1024):
-    """The device-resident forward pass (em_model) at
-    Llama-2-7B dimensions, n_layers deep, int8 weights (random ~N(0, 0.02),
-    drawn on the GPU): a 512-token prefill, then greedy decode steps from
-    position 512, each a host call that returns the logits (graph replay)."""
+def llama7b_model(em, torch, n_layers: int = 2, n_kv_heads: int = 32, seq_len: int = 1024):
+    """An em_model at Llama-2-7B dimensions, n_layers deep, int8 weights
+    (random ~N(0, 0.02), drawn on the GPU, embedding ~N(0, 1), norm gains 1)."""
     import numpy as np
     D, H, V, heads = 4096, 11008, 32000, 32
     KV = n_kv_heads * (D // heads)
@@ -225,10 +223,17 @@ def llama7b_model_case(em, torch, n_layers: int = 2, n_kv_heads: int = 32, seq_l
                    w13=rnd(D, 2 * H), w2=rnd(H, D)) for _ in range(n_layers)]
     cfg = dict(dim=D, hidden_dim=H, n_layers=n_layers, n_heads=heads, n_kv_heads=n_kv_heads,
                vocab_size=V, seq_len=seq_len)
-    model = em.Model(cfg, dict(token_embedding=rnd(V, D, std=1.0), rms_final=ones,
-                               wcls=rnd(D, V), layers=layers), q8=True)
-    del layers
-    prompt = [(7 * i + 3) % V for i in range(512)]
+    return em.Model(cfg, dict(token_embedding=rnd(V, D, std=1.0), rms_final=ones,
+                              wcls=rnd(D, V), layers=layers), q8=True)
+
+
+def llama7b_model_case(em, torch, n_layers: int = 2, n_kv_heads: int = 32, seq_len: int = 1024):
+    """The device-resident forward pass (em_model) at Llama-2-7B dimensions
+    (llama7b_model): a 512-token prefill, then greedy decode steps from
+    position 512, each a host call that returns the logits (graph replay)."""
+    import numpy as np
+    model = llama7b_model(em, torch, n_layers, n_kv_heads, seq_len)
+    prompt = [(7 * i + 3) % 32000 for i in range(512)]
     model.forward(prompt, 0)  # warm-up: grows every buffer
     t0 = time.perf_counter()
     reps = 3
@@ -419,6 +424,17 @@ def profile_split_pass(em, torch, m: int = 512, reps: int = 20) -> dict:
     return {"m": m, "launches": reps, "flops_per_launch": 2 * m * DIM * DIM}
 
 
+def profile_prefill_pass(em, torch, reps: int = 5) -> dict:
+    """Eager 512-token prefills of the two-layer Llama-7B-shaped model
+    (llama7b_model), for rocprofv3 kernel traces of the forward pass."""
+    model = llama7b_model(em, torch)
+    prompt = [(7 * i + 3) % 32000 for i in range(512)]
+    for _ in range(reps):
+        model.forward(prompt, 0)
+    model.close()
+    return {"layers": 2, "prefill_tokens": 512, "calls": reps}
+
+
 def measured_traffic():
     """HBM bytes per headline call from the committed counter summary, or None."""
     path = os.path.join(ROOT, "profiles", "gemv_int8_m1_4096_traffic.json")
@@ -474,10 +490,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
-    ap.add_argument("--profile-pass", nargs="?", const="gemv", choices=["gemv", "gemm", "split"],
+    ap.add_argument("--profile-pass", nargs="?", const="gemv", choices=["gemv", "gemm", "split", "prefill"],
                     help="eager launches for rocprofv3 --pmc: gemv (calibration copy + "
-                         "headline, the default), gemm (fp32 tiled N=4096) or split "
-                         "(int8 m=512, exact-split)")
+                         "headline, the default), gemm (fp32 tiled N=4096), split "
+                         "(int8 m=512, exact-split) or prefill (Llama-7B-shaped, 2 layers)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -496,6 +512,9 @@ def main() -> int:
         return 0
     if args.profile_pass == "split":
         print(json.dumps(profile_split_pass(em, torch)))
+        return 0
+    if args.profile_pass == "prefill":
+        print(json.dumps(profile_prefill_pass(em, torch)))
         return 0
     if args.profile_pass:
         print(json.dumps(profile_pass(em, torch)))
