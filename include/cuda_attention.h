@@ -25,7 +25,7 @@ struct AttentionShape {
 
 // cuda_attention.h:15-19.
 enum class AttentionKernel {
-    automatic = EM_ATTN_AUTOMATIC,        // split for few rows; one chunk per row for many
+    automatic = EM_ATTN_AUTOMATIC,        // split for few rows; 16-row MFMA tiles for many
     single_block = EM_ATTN_SINGLE_BLOCK,  // one workgroup per (head, row), scores in LDS
     split = EM_ATTN_SPLIT,                // positions split across workgroups, then merged
 };
