@@ -435,6 +435,19 @@ def profile_prefill_pass(em, torch, reps: int = 5) -> dict:
     return {"layers": 2, "prefill_tokens": 512, "calls": reps}
 
 
+def profile_decode_pass(em, torch, steps: int = 20) -> dict:
+    """A 512-token prefill of the two-layer Llama-7B-shaped model, then
+    `steps` greedy decode calls (graph replays), for kernel traces."""
+    import numpy as np
+    model = llama7b_model(em, torch)
+    prompt = [(7 * i + 3) % 32000 for i in range(512)]
+    tok = int(np.argmax(model.forward(prompt, 0)))
+    for i in range(steps):
+        tok = int(np.argmax(model.forward(tok, 512 + i)))
+    model.close()
+    return {"layers": 2, "decode_calls": steps, "context": 512}
+
+
 def measured_traffic():
     """HBM bytes per headline call from the committed counter summary, or None."""
     path = os.path.join(ROOT, "profiles", "gemv_int8_m1_4096_traffic.json")
@@ -443,6 +456,45 @@ def measured_traffic():
             return json.load(f)
     except (OSError, ValueError):
         return None
+
+
+def hbm_ceiling(em, torch, nbytes: int = POOL_MIN_BYTES, reps: int = 5) -> dict:
+    """What plain streaming reaches on this GPU, beside the GEMV: a device to
+    device copy (the reference's ceiling, bench_cuda.cpp:79-88; bytes read +
+    written), the library's read-only stream (em_stream_read) and torch's
+    sum, each over a buffer past the 256 MB Infinity Cache, timed with HIP
+    events on torch's stream."""
+    src = torch.ones(nbytes // 4, device="cuda", dtype=torch.float32)
+    dst = torch.empty_like(src)
+    sink = torch.zeros(1, device="cuda", dtype=torch.int32)
+    out = {}
+    for name, op, moved in (("d2d_copy", lambda: dst.copy_(src), 2 * nbytes),
+                            ("read_stream", lambda: em.stream_read(src, sink), nbytes),
+                            ("read_sum", lambda: src.sum(), nbytes)):
+        op()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            op()
+        e1.record()
+        torch.cuda.synchronize()
+        secs = e0.elapsed_time(e1) / 1e3 / reps
+        out[name + "_GBps"] = round(moved / secs / 1e9, 1)
+    out["buffer_MiB"] = nbytes >> 20
+    del src, dst
+    return out
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_threads() -> int:
@@ -473,7 +525,8 @@ def cpu_baseline(A_dev, q_dev, s_dev, gemm_AB):
            "sample": f"int8 GEMV m=1 4096x4096 (one W, no rotation), matmul_parallel, "
                      f"median of {reps} reps after 1 warm-up",
            "ms": secs * 1e3, "compiler": ref.compiler().split("(")[0].strip(),
-           "library": os.path.basename(ref.path), "pool_threads": ref.pool_size()}
+           "library": os.path.basename(ref.path), "pool_threads": ref.pool_size(),
+           "cpu_model": cpu_model(), "nproc": os.cpu_count()}
     if gemm_AB is not None:
         Ah = gemm_AB[0].cpu().numpy()
         Bh = gemm_AB[1].cpu().numpy()
@@ -490,10 +543,15 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
-    ap.add_argument("--profile-pass", nargs="?", const="gemv", choices=["gemv", "gemm", "split", "prefill"],
+    ap.add_argument("--llama7b-layers", type=int, default=0, metavar="L",
+                    help="only time the Llama-7B-shaped forward pass L layers deep (32 for "
+                         "the full model; builds ~0.8 GB of host weights per layer) and print "
+                         "its JSON line")
+    ap.add_argument("--profile-pass", nargs="?", const="gemv", choices=["gemv", "gemm", "split", "prefill", "decode"],
                     help="eager launches for rocprofv3 --pmc: gemv (calibration copy + "
                          "headline, the default), gemm (fp32 tiled N=4096), split "
-                         "(int8 m=512, exact-split) or prefill (Llama-7B-shaped, 2 layers)")
+                         "(int8 m=512, exact-split), prefill or decode (Llama-7B-shaped, "
+                         "2 layers)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -507,6 +565,18 @@ def main() -> int:
     if not torch.cuda.is_available() or not em.available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
+    if args.llama7b_layers:
+        out = {"metric": "Llama-7B-shaped forward pass through em_model", "n_gpus": 1,
+               "data": "synthetic: random int8-quantised weights, fixed prompt"}
+        for kv in (32, 8):
+            t0 = time.perf_counter()
+            r = llama7b_model_case(em, torch, n_layers=args.llama7b_layers, n_kv_heads=kv)
+            r["wall_s_with_setup"] = round(time.perf_counter() - t0, 1)
+            out["mha" if kv == 32 else "gqa8"] = r
+            print(json.dumps({"done": "mha" if kv == 32 else "gqa8", **r}), file=sys.stderr,
+                  flush=True)
+        print(json.dumps(out))
+        return 0
     if args.profile_pass == "gemm":
         print(json.dumps(profile_gemm_pass(em, torch)))
         return 0
@@ -516,11 +586,15 @@ def main() -> int:
     if args.profile_pass == "prefill":
         print(json.dumps(profile_prefill_pass(em, torch)))
         return 0
+    if args.profile_pass == "decode":
+        print(json.dumps(profile_decode_pass(em, torch)))
+        return 0
     if args.profile_pass:
         print(json.dumps(profile_pass(em, torch)))
         return 0
 
     head, (A1, _) = gemv_case(em, torch, 1, True, args.steps, args.warmup)
+    ceiling = hbm_ceiling(em, torch)
     steps = args.steps
     secs = head["secs"]
     avg_launch_s = secs / head["calls"]
@@ -553,7 +627,12 @@ def main() -> int:
                      "kernel": "gemv_kernel<int8,1,16,16> + reduce_slices (one em_matmul_q8 call: "
                                "split-K partials, then the fixed-order slice sum)",
                      "avg_launch_us": round(avg_launch_s * 1e6, 3),
-                     "bytes_per_launch": head["bytes_per_call"]},
+                     "bytes_per_launch": head["bytes_per_call"],
+                     "achievable_read_GBps": ceiling["read_stream_GBps"],
+                     "frac_of_achievable": round(achieved / ceiling["read_stream_GBps"], 4),
+                     "achievable_note": "em_stream_read over a 600 MiB buffer in the same run "
+                                        "(device-to-device copy: "
+                                        f"{ceiling['d2d_copy_GBps']} GB/s read + write)"},
     }
 
     extra = {}
@@ -582,6 +661,7 @@ def main() -> int:
         extra["stories15m_forward"] = stories15m_case(em, torch)
         extra["llama7b_model_2layers_int8"] = llama7b_model_case(em, torch)
         extra["llama7b_model_2layers_int8_gqa8"] = llama7b_model_case(em, torch, n_kv_heads=8)
+        extra["hbm_ceiling"] = ceiling
         # The reference's own convention (bench_cuda.cpp:41-54): host time of
         # one launch -> synchronize, median of 101, one W (cache-resident).
         pool = Pool(em, torch, True, DIM, DIM, 1, 99)

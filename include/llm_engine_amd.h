@@ -98,6 +98,13 @@ int em_quantize_q8(size_t rows, size_t cols, const float* B, int8_t* q, float* s
 int em_dequantize_q8(size_t rows, size_t cols, const int8_t* q, const float* scale, float* out,
                      void* stream);
 
+/* Reads `bytes` of device memory at `buf` once (both multiples of 16), the
+ * read-only HBM ceiling that bench.py reports beside the GEMV. No counterpart
+ * in the reference, whose bench times a device-to-device copy as its ceiling
+ * (bench_cuda.cpp:79-88); it is for callers that measure the matmul path.
+ * `sink` is 4 bytes of device memory the kernel may write (almost never). */
+int em_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream);
+
 /* ---- Causal attention over a KV cache (cuda_attention.h) ------------------ */
 
 /* Replaces struct AttentionShape, cuda_attention.h:8-13. */

@@ -28,7 +28,7 @@ STREAM_PER_THREAD = 2
 EXPORTS = (
     "em_last_error", "em_available", "em_synchronize", "em_scratch_generation",
     "em_malloc", "em_free", "em_memcpy_h2d", "em_memcpy_d2h",
-    "em_matmul_f32", "em_matmul_q8", "em_quantize_q8", "em_dequantize_q8",
+    "em_matmul_f32", "em_matmul_q8", "em_quantize_q8", "em_dequantize_q8", "em_stream_read",
     "em_attention_check", "em_attention_scratch_floats", "em_attention",
     "em_model_create", "em_model_destroy", "em_model_forward",
 )
@@ -116,6 +116,7 @@ def lib() -> ctypes.CDLL:
                                    ctypes.c_int, _vp, _vp]
         L.em_quantize_q8.argtypes = [_sz, _sz, _vp, _vp, _vp, _vp]
         L.em_dequantize_q8.argtypes = [_sz, _sz, _vp, _vp, _vp, _vp]
+        L.em_stream_read.argtypes = [_vp, _sz, _vp, _vp]
         shp = ctypes.POINTER(AttentionShape)
         L.em_attention_check.argtypes = [shp, ctypes.c_int]
         L.em_attention_scratch_floats.argtypes = [shp, _sz, ctypes.c_int]
@@ -227,6 +228,13 @@ def quantize_q8(B, stream=None):
     quantize_q8_raw(rows, cols, _dev(B, torch.float32), _dev(q, torch.int8),
                     _dev(scale, torch.float32), _stream_ptr(stream))
     return q, scale
+
+
+def stream_read(buf, sink, stream=None) -> None:
+    """One read-only pass over a device tensor (its bytes a multiple of 16)
+    on torch's current stream; sink is a 1-element int32 device tensor."""
+    _check(lib().em_stream_read(buf.data_ptr(), buf.numel() * buf.element_size(),
+                                sink.data_ptr(), _stream_ptr(stream)))
 
 
 def dequantize_q8(q, scale, stream=None):

@@ -280,6 +280,21 @@ int em_dequantize_q8(size_t rows, size_t cols, const int8_t* q, const float* sca
 }
 
 
+int em_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream) {
+    if (bytes == 0) return EM_OK;
+    if (!buf || !sink) return fail(EM_EINVAL, "stream_read: null pointer");
+    if (bytes % 16 || reinterpret_cast<uintptr_t>(buf) % 16)
+        return fail(EM_EINVAL, "stream_read: buffer and size must be multiples of 16 bytes");
+    if (!em::device_present()) return fail(EM_ENODEV, "stream_read: no usable GPU");
+    try {
+        em::run_stream_read(buf, bytes, sink, static_cast<hipStream_t>(stream));
+        em::hip_check(hipGetLastError(), "launch");
+    } catch (const std::exception& e) {
+        return fail(EM_EDEVICE, e.what());
+    }
+    return EM_OK;
+}
+
 static em::AttnShape to_shape(const em_attention_shape& s) {
     return {s.n_heads, s.n_kv_heads, s.head_size, s.seq_len, s.q_stride, s.kv_stride, s.out_stride};
 }

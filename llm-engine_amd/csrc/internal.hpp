@@ -81,6 +81,8 @@ void run_reduce_slices(int m, int n, int slices, const float* partial, const flo
 
 // Zero `count` floats with a kernel (not hipMemsetAsync, so graph capture is safe).
 void run_fill_zero(float* p, std::size_t count, hipStream_t stream);
+// Reads bytes (a multiple of 16) of buf once, 16-byte aligned.
+void run_stream_read(const void* buf, std::size_t bytes, uint32_t* sink, hipStream_t stream);
 
 void run_quantize_q8(int rows, int cols, const float* B, int8_t* q, float* scale,
                      hipStream_t stream);

@@ -114,3 +114,15 @@ def test_attention_check_rejects_like_the_reference():
     assert rejects(S(4, 4, 8, 64, 64, 32, 32), 7)              # unknown kernel
     assert em.attention_scratch_floats(S(4, 4, 8, 64, 64, 32, 32), 3, "single_block") == 0
     assert em.attention_scratch_floats(S(4, 4, 8, 64, 64, 32, 32), 3, "split") > 0
+
+
+def test_stream_read_checks_before_the_gpu():
+    # Size and alignment are rejected on the host, GPU or not; zero bytes is
+    # a no-op.
+    em = engine.load()
+    L = em.lib()
+    assert L.em_stream_read(None, 0, None, None) == em.EM_OK
+    assert L.em_stream_read(None, 16, 16, None) == em.EM_EINVAL
+    assert L.em_stream_read(16, 24, 16, None) == em.EM_EINVAL
+    assert b"multiples of 16" in L.em_last_error()
+    assert L.em_stream_read(8, 32, 16, None) == em.EM_EINVAL

@@ -356,3 +356,14 @@ def test_exact_split_fused_norm_and_accumulate():
     em.matmul(dev(A), dev(q), C, scale=dev(s), accumulate=True, rms_weight=dev(w))
     An = orc.rmsnorm(A, w)
     check(host(C), want, An, orc.dequantize(q, s), k, factor=2.0, C0=C0)
+
+
+def test_stream_read_runs_and_checks_alignment():
+    # The bench's read-only ceiling: one pass over a buffer, nothing written
+    # but (almost never) the sink.
+    buf = torch.ones(1 << 20, device="cuda")
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    em.stream_read(buf, sink)
+    torch.cuda.synchronize()
+    with pytest.raises(em.InvalidArgument):
+        em.stream_read(buf[1:5], sink)  # 4-byte offset
