@@ -322,7 +322,7 @@ int rows_per_lane(int E, int m, int n, int k) {
 }  // namespace
 
 template <class BT>
-void run_skinny(const MatmulArgs& a) {
+int run_skinny_partials(const MatmulArgs& a, const float** partial) {
     const BT* B = static_cast<const BT*>(a.B);
     int E = 1;
     if (std::is_same<BT, int8_t>::value && a.n % 16 == 0 && aligned(B, 16)) {
@@ -352,12 +352,22 @@ void run_skinny(const MatmulArgs& a) {
     } else {
         pick_width<BT, false>(E, L, p, grid, a.stream);
     }
-    if (!p.direct)
-        run_reduce_slices(a.m, a.n, slices, p.out,
+    *partial = p.direct ? nullptr : p.out;
+    return slices;
+}
+
+template <class BT>
+void run_skinny(const MatmulArgs& a) {
+    const float* partial = nullptr;
+    const int slices = run_skinny_partials<BT>(a, &partial);
+    if (slices > 1)
+        run_reduce_slices(a.m, a.n, slices, partial,
                           std::is_same<BT, int8_t>::value ? a.scale : nullptr, a.C,
                           a.accumulate, a.stream);
 }
 
+template int run_skinny_partials<float>(const MatmulArgs&, const float**);
+template int run_skinny_partials<int8_t>(const MatmulArgs&, const float**);
 template void run_skinny<float>(const MatmulArgs&);
 template void run_skinny<int8_t>(const MatmulArgs&);
 

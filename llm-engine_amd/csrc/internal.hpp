@@ -47,6 +47,13 @@ struct MatmulArgs {
 // Decode-shaped GEMV, m <= 8 (GpuKernel::skinny). Fuses the norm.
 template <class BT>
 void run_skinny(const MatmulArgs& a);
+// The same GEMV without its slice sum: returns the number of k slices. With
+// one slice C is written (scaled, accumulated) as run_skinny writes it;
+// with more, *partial holds [slice][m][n] unscaled sums (library scratch)
+// that the caller must add in slice order, scale and store exactly as
+// reduce_slices does (a consumer kernel that fuses the sum).
+template <class BT>
+int run_skinny_partials(const MatmulArgs& a, const float** partial);
 
 // MFMA over 16/32/64-row tiles with B streamed once and k split across
 // blocks (GpuKernel::tiled_split). A must already be normed.

@@ -13,6 +13,10 @@
 //   x += swiglu(gu) W2                              swiglu_kernel, product
 // then logits = rmsnorm(x[last]) Wcls. The products are this library's
 // matmul entry, so they pick the same kernels a caller of em_matmul_* gets.
+// At decode sizes (m <= 8) the qkv and w13 GEMVs leave their k-slice
+// partials to rope_cache_kernel and swiglu_kernel, which add them in slice
+// order and scale them exactly as reduce_slices would: the same bits, two
+// dependent launches fewer per layer.
 //
 // Kernels read the position and tokens from the device feed, so the first
 // one-token call is run eagerly and then captured into a HIP graph that
@@ -33,6 +37,25 @@
 namespace em {
 namespace {
 
+// A product's output as its consumer reads it: C itself (one k slice, or a
+// kernel that writes C), or the skinny GEMV's partials [slice][m][n] summed
+// in slice order and scaled by the column scale: reduce_slices' arithmetic.
+struct Summed {
+    const float* c;
+    const float* partial;
+    const float* scale;  // int8 column scales, null for fp32
+    int slices, n;
+    std::size_t mn;
+};
+
+__device__ __forceinline__ float summed(const Summed& s, int row, int col) {
+    const std::size_t idx = static_cast<std::size_t>(row) * s.n + col;
+    if (s.slices == 1) return s.c[idx];
+    float t = ordered_sum(s.partial + idx, s.mn, s.slices);
+    if (s.scale) t *= s.scale[col];
+    return t;
+}
+
 // x[i] = table[feed[1 + i]], one workgroup per row (the reference's embed,
 // cuda_model.cu:26-31). Token ids were range-checked on the host.
 __global__ __launch_bounds__(kThreads) void embed_kernel(int dim, const int* feed,
@@ -45,30 +68,29 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(int dim, const int* fee
 // Row blockIdx.y, at position feed[0] + blockIdx.y: rotates each (even, odd)
 // pair of q and k by the position's angles, as rope() does (model.cpp:93-103),
 // then writes the rotated k and the v slice into the caches (model.cpp:297-
-// 299). A thread takes one q pair, one k pair or one v element.
-__global__ __launch_bounds__(kThreads) void rope_cache_kernel(int qkv_cols, int dim, int kv_dim,
-                                                              int head_size, const int* feed,
-                                                              const float* cos_t,
+// 299). A thread takes one q pair, one k pair or one v element; src yields
+// the qkv product (qkv_cols wide), which is stored back to qkv rotated.
+__global__ __launch_bounds__(kThreads) void rope_cache_kernel(Summed src, int qkv_cols, int dim,
+                                                              int kv_dim, int head_size,
+                                                              const int* feed, const float* cos_t,
                                                               const float* sin_t, float* qkv,
                                                               float* key_cache,
                                                               float* value_cache) {
     const int i = blockIdx.y, pos = feed[0] + i, half = head_size / 2;
-    float* q = qkv + static_cast<std::size_t>(i) * qkv_cols;
-    float* k = q + dim;
-    const float* v = k + kv_dim;
+    float* row = qkv + static_cast<std::size_t>(i) * qkv_cols;
     const int nq = dim / 2, nk = kv_dim / 2;
     const int j = blockIdx.x * kThreads + threadIdx.x;
     if (j < nq + nk) {
         const bool is_k = j >= nq;
         const int pair = is_k ? j - nq : j;
-        float* p = (is_k ? k : q) + 2 * pair;
+        const int col = (is_k ? dim : 0) + 2 * pair;
         const int a = pos * half + pair % half;
         const float c = cos_t[a], s = sin_t[a];
-        const float x0 = p[0], x1 = p[1];
+        const float x0 = summed(src, i, col), x1 = summed(src, i, col + 1);
         const float y0 = x0 * c - x1 * s;
         const float y1 = x0 * s + x1 * c;
-        p[0] = y0;
-        p[1] = y1;
+        row[col] = y0;
+        row[col + 1] = y1;
         if (is_k) {
             float* dst = key_cache + static_cast<std::size_t>(pos) * kv_dim + 2 * pair;
             dst[0] = y0;
@@ -76,19 +98,22 @@ __global__ __launch_bounds__(kThreads) void rope_cache_kernel(int qkv_cols, int 
         }
     } else if (j < nq + nk + kv_dim) {
         const int t = j - nq - nk;
-        value_cache[static_cast<std::size_t>(pos) * kv_dim + t] = v[t];
+        const float val = summed(src, i, dim + kv_dim + t);
+        row[dim + kv_dim + t] = val;
+        value_cache[static_cast<std::size_t>(pos) * kv_dim + t] = val;
     }
 }
 
-// hb[r][c] = silu(gu[r][c]) * gu[r][hidden + c] (model.cpp:306-310).
-__global__ __launch_bounds__(kThreads) void swiglu_kernel(int rows, int hidden, const float* gu,
+// hb[r][c] = silu(g) * u with g = gu[r][c], u = gu[r][hidden + c]
+// (model.cpp:306-310); src yields the w13 product (2 * hidden wide).
+__global__ __launch_bounds__(kThreads) void swiglu_kernel(int rows, int hidden, Summed src,
                                                           float* hb) {
     const int total = rows * hidden;
     for (int idx = blockIdx.x * kThreads + threadIdx.x; idx < total;
          idx += gridDim.x * kThreads) {
         const int r = idx / hidden, c = idx % hidden;
-        const float g = gu[static_cast<std::size_t>(r) * 2 * hidden + c];
-        hb[idx] = g / (1.0f + expf(-g)) * gu[static_cast<std::size_t>(r) * 2 * hidden + hidden + c];
+        const float g = summed(src, r, c);
+        hb[idx] = g / (1.0f + expf(-g)) * summed(src, r, hidden + c);
     }
 }
 
@@ -185,6 +210,7 @@ private:
     void make_proj(Proj& p, const float* w, int rows, int cols, Buf<float>& staging);
     void project(int n, const float* in, const Proj& w, float* out, const float* rms,
                  bool accumulate);
+    Summed project_summed(int n, const float* in, const Proj& w, float* out, const float* rms);
     void reserve_rows(std::size_t n);
     void enqueue(int n);
     std::size_t buffers_generation() const { return own_generation_ + scratch_generation(); }
@@ -297,6 +323,37 @@ void Model::project(int n, const float* in, const Proj& w, float* out, const flo
     if (rc != EM_OK) throw DeviceError(em_last_error());
 }
 
+// out = rmsnorm(in) W for a consumer that reads it through summed(): at
+// decode sizes the skinny GEMV leaves its k-slice partials (no reduce
+// launch), otherwise the product is written to out as project() does.
+Summed Model::project_summed(int n, const float* in, const Proj& w, float* out,
+                             const float* rms) {
+    Summed s{out, nullptr, nullptr, 1, w.cols, static_cast<std::size_t>(n) * w.cols};
+    if (n > 8) {
+        project(n, in, w, out, rms, false);
+        return s;
+    }
+    MatmulArgs a{};
+    a.m = n;
+    a.n = w.cols;
+    a.k = w.rows;
+    a.A = in;
+    a.B = q8_ ? static_cast<const void*>(w.q8.p) : static_cast<const void*>(w.f32.p);
+    a.scale = q8_ ? w.scale.p : nullptr;
+    a.C = out;
+    a.accumulate = false;
+    a.rms_weight = rms;
+    a.stream = stream_;
+    const float* partial = nullptr;
+    s.slices = q8_ ? run_skinny_partials<int8_t>(a, &partial) : run_skinny_partials<float>(a, &partial);
+    check(hipGetLastError(), "launch");
+    if (s.slices > 1) {
+        s.partial = partial;
+        s.scale = a.scale;
+    }
+    return s;
+}
+
 void Model::reserve_rows(std::size_t n) {
     if (n <= rows_) return;
     check(hipStreamSynchronize(stream_), "synchronize before growth");
@@ -324,16 +381,16 @@ void Model::enqueue(int n) {
     const int rope_threads = D / 2 + KV / 2 + KV;
     const int swiglu_blocks = std::min(ceil_div(static_cast<long long>(n) * H, kThreads), 4096);
     for (LayerDev& L : layers_) {
-        project(n, x_.p, L.wqkv, qkv_.p, L.rms_att.p, false);
+        const Summed qkv = project_summed(n, x_.p, L.wqkv, qkv_.p, L.rms_att.p);
         hipLaunchKernelGGL(rope_cache_kernel, dim3(ceil_div(rope_threads, kThreads), n),
-                           dim3(kThreads), 0, stream_, qkv_cols, D, KV, hs, feed_dev_.p,
+                           dim3(kThreads), 0, stream_, qkv, qkv_cols, D, KV, hs, feed_dev_.p,
                            rope_cos_.p, rope_sin_.p, qkv_.p, L.kcache.p, L.vcache.p);
         run_attention(shape_, n, feed_dev_.p, qkv_.p, L.kcache.p, L.vcache.p, att_.p,
                       attn_scratch_.p, kAttnAutomatic, stream_);
         project(n, att_.p, L.wo, x_.p, nullptr, true);
-        project(n, x_.p, L.w13, gu_.p, L.rms_ffn.p, false);
+        const Summed gu = project_summed(n, x_.p, L.w13, gu_.p, L.rms_ffn.p);
         hipLaunchKernelGGL(swiglu_kernel, dim3(swiglu_blocks), dim3(kThreads), 0, stream_, n, H,
-                           gu_.p, hb_.p);
+                           gu, hb_.p);
         project(n, hb_.p, L.w2, x_.p, nullptr, true);
     }
     // Only the last row's logits are returned.
