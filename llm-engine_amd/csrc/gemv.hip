@@ -131,6 +131,25 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
     const bool active = col < p.n;
     const int p0 = blockIdx.y * R;
 
+    // With a norm: the first NP values of each row this thread sums squares
+    // of (k = tid, tid + 256, ...), loaded before the weight loads. A loop
+    // of loads after them would wait for the whole weight stream at its
+    // first s_waitcnt and then take one L2 round trip per step.
+    constexpr int NP = !NORM ? 1 : MM == 1 ? 32 : MM == 2 ? 16 : MM <= 4 ? 4 : 2;
+    // Loads are unconditional (addresses clamped into A; k >= 1 here) so
+    // that no branch separates them; values past m or k are masked at use.
+    float npre[MM][NP];
+    if constexpr (NORM) {
+#pragma unroll
+        for (int r = 0; r < MM; ++r)
+#pragma unroll
+            for (int i = 0; i < NP; ++i) {
+                const int rr = r < p.m ? r : p.m - 1;
+                const int j = min(tid + i * kThreads, p.k - 1);
+                npre[r][i] = p.A[rr * p.k + j];
+            }
+    }
+
     // This workgroup's slice of A, raw, into registers: issued before the
     // weight loads so its wait does not include them.
     float a_reg[AREG];
@@ -153,13 +172,23 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
         const int pp = min(p0 + rg + i * E, p.k - 1);
         w[i] = LT::load(p.B + static_cast<uint32_t>(pp * p.n + lcol));
     }
+    // Nothing that uses a loaded value is moved above the loads.
+    __builtin_amdgcn_sched_barrier(0);
 
     if constexpr (NORM) {
 #pragma unroll
         for (int r = 0; r < MM; ++r) {
+            // The same sequence of fmaf as a plain loop over j: the
+            // preloaded values (zero past k adds exactly nothing), then any
+            // rest of the row.
             float ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NP; ++i) {
+                const float v = (r < p.m && tid + i * kThreads < p.k) ? npre[r][i] : 0.0f;
+                ss = fmaf(v, v, ss);
+            }
             if (r < p.m)
-                for (int j = tid; j < p.k; j += kThreads) {
+                for (int j = tid + NP * kThreads; j < p.k; j += kThreads) {
                     const float v = p.A[r * p.k + j];
                     ss = fmaf(v, v, ss);
                 }
