@@ -539,6 +539,11 @@ def cpu_baseline(A_dev, q_dev, s_dev, gemm_AB):
     return out
 
 
+def progress(msg: str) -> None:
+    """A stage line on stderr (stdout carries only the result line)."""
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[1])
     ap.add_argument("--gpus", type=int, default=1)
@@ -659,11 +664,16 @@ def main() -> int:
         gemm, gemm_AB = gemm_case(em, torch)
         extra["fp32_gemm_N4096"] = {k: round(v, 3) if isinstance(v, float) else v
                                     for k, v in gemm.items()}
+        progress("gemv and gemm legs done")
         extra["llama7b_layer_int8"] = llama7b_case(em, torch, steps)
+        progress("llama7b layer done")
         extra["decode_attention"] = attention_case(em, torch)
+        progress("attention done")
         extra["stories15m_forward"] = stories15m_case(em, torch)
+        progress("stories15M done")
         extra["llama7b_model_2layers_int8"] = llama7b_model_case(em, torch)
         extra["llama7b_model_2layers_int8_gqa8"] = llama7b_model_case(em, torch, n_kv_heads=8)
+        progress("llama7b models done")
         extra["hbm_ceiling"] = ceiling
         # The reference's own convention (bench_cuda.cpp:41-54): host time of
         # one launch -> synchronize, median of 101, one W (cache-resident).
