@@ -320,7 +320,10 @@ def test_config3_square_gemm(N):
 # planes), and m and n that end inside a tile.
 SPLIT_SHAPES = [(9, 300, 32), (12, 4096, 4096), (24, 4096, 4096), (64, 4096, 4096), (100, 777, 272),
                 (512, 4096, 512), (33, 1029, 256), (64, 31, 48), (300, 4096, 256), (1024, 1024, 512),
-                (1040, 520, 272), (1100, 301, 160)]
+                (1040, 520, 272), (1100, 301, 160),
+                # wide products, with k whole chunks or ragged, A split in
+                # registers or pre-split, m ending inside a tile
+                (512, 4096, 12288), (300, 520, 12288), (200, 301, 32768), (2048, 1024, 4096)]
 
 
 @pytest.mark.parametrize("shape", SPLIT_SHAPES, ids=lambda s: "x".join(map(str, s)))
@@ -345,8 +348,10 @@ def test_exact_split_tighter_than_fp32_tolerance(shape):
         assert ratio <= 1e-5, (kernel, ratio)
 
 
-def test_exact_split_fused_norm_and_accumulate():
-    m, k, n = 40, 1000, 304
+@pytest.mark.parametrize("shape", [(40, 1000, 304), (256, 1000, 16384)], ids=lambda s: "x".join(map(str, s)))
+def test_exact_split_fused_norm_and_accumulate(shape):
+    # A narrow product split across k, and a wide one.
+    m, k, n = shape
     A = inputs.normal((m, k), 1.0, 511)
     w = inputs.uniform((k,), 0.5, 1.5, 512)
     C0 = inputs.normal((m, n), 1.0, 513)
