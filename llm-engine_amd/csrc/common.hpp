@@ -100,6 +100,29 @@ __device__ __forceinline__ float ordered_sum(const float* p, size_t stride, int 
     return total;
 }
 
+// A product's output as a consumer reads it: C itself (one k slice, or a
+// kernel that writes C), or the skinny GEMV's partials [slice][m][n] summed
+// in slice order and scaled by the column scale: reduce_slices' arithmetic.
+struct Summed {
+    const float* c;
+    const float* partial;
+    const float* scale;  // int8 column scales, null for fp32
+    int slices, n;
+    size_t mn;
+};
+
+__device__ __forceinline__ float summed(const Summed& s, int row, int col) {
+    const size_t idx = static_cast<size_t>(row) * s.n + col;
+    if (s.slices == 1) return s.c[idx];
+    float t = ordered_sum(s.partial + idx, s.mn, s.slices);
+    if (s.scale) t *= s.scale[col];
+    return t;
+}
+
+// SwiGLU of one (gate, up) pair, silu(g) * u (model.cpp:306-310): the one
+// expression every kernel that forms it uses, so they agree bit for bit.
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
 // Tile of workgroup `id` of a 1-D grid. Workgroups are dispatched to the
 // eight XCDs in turn (id % 8), each XCD with its own L2. With xcd_order the
 // ids are renumbered so that each XCD receives a contiguous run of tiles,

@@ -106,11 +106,20 @@ struct GemvParams {
     int accumulate;
     int direct;
     int a_vec4;          // k % 4 == 0 and A 16-byte aligned: the norm reads float4
+    Summed gu;           // SWI: the w13 product A is formed from
+    int hidden;          // SWI: its gate | up split
 };
+
+// Slices a SwiGLU source may have: its values are loaded into registers.
+constexpr int kSwiSlices = 16;
 
 // MM: rows of A the kernel is compiled for (m <= MM; extra rows are zero).
 // E: columns per lane. L: rows per lane. NORM: fused RMSNorm of A.
-template <class BT, int MM, int E, int L, bool NORM>
+// SWI (one row, at most 256 rows of k per workgroup): A is not read but
+// formed, A[j] = silu_mul(gate[j], up[j]) of a product given as a Summed
+// (p.gu, gate | up at p.hidden): the arithmetic of the forward pass's SwiGLU
+// kernel, so the result is the same as running that kernel first.
+template <class BT, int MM, int E, int L, bool NORM, bool SWI = false>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
     using LT = Lane<BT, E>;
     using V = typename LT::V;
@@ -168,11 +177,30 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
     // This workgroup's slice of A, raw, into registers: issued before the
     // weight loads so its wait does not include them.
     float a_reg[AREG];
+    float sg[SWI ? kSwiSlices : 1], su[SWI ? kSwiSlices : 1];
+    if constexpr (SWI) {
+        static_assert(MM == 1 && AREG == 1 && !NORM, "SwiGLU source: one row, one value per thread");
+        // Gate and up of this thread's k index, every slice (clamped past
+        // the last; only the first gu.slices are added).
+        const int col = min(p0 + tid % R, p.k - 1);
+        if (p.gu.slices == 1) {
+            sg[0] = p.gu.c[col];
+            su[0] = p.gu.c[p.hidden + col];
+        } else {
 #pragma unroll
-    for (int t = 0; t < AREG; ++t) {
-        const int idx = tid + t * kThreads;
-        const int r = idx / R, pp = p0 + idx % R;
-        a_reg[t] = (idx < MM * R && r < p.m && pp < p.k) ? p.A[r * p.k + pp] : 0.0f;
+            for (int sl = 0; sl < kSwiSlices; ++sl) {
+                const size_t off = static_cast<size_t>(min(sl, p.gu.slices - 1)) * p.gu.mn + col;
+                sg[sl] = p.gu.partial[off];
+                su[sl] = p.gu.partial[off + p.hidden];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < AREG; ++t) {
+            const int idx = tid + t * kThreads;
+            const int r = idx / R, pp = p0 + idx % R;
+            a_reg[t] = (idx < MM * R && r < p.m && pp < p.k) ? p.A[r * p.k + pp] : 0.0f;
+        }
     }
 
     // All L weight vectors of this lane in flight at once. No load is
@@ -190,6 +218,27 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
     // Nothing that uses a loaded value is moved above the loads.
     __builtin_amdgcn_sched_barrier(0);
 
+    if constexpr (SWI) {
+        // summed(): C as is, or the slices added in order, then the scale.
+        const int col = min(p0 + tid % R, p.k - 1);
+        float g = sg[0], u = su[0];
+        if (p.gu.slices > 1) {
+            g = 0.0f;
+            u = 0.0f;
+#pragma unroll
+            for (int sl = 0; sl < kSwiSlices; ++sl) {
+                if (sl < p.gu.slices) {
+                    g += sg[sl];
+                    u += su[sl];
+                }
+            }
+            if (p.gu.scale) {
+                g *= p.gu.scale[col];
+                u *= p.gu.scale[p.hidden + col];
+            }
+        }
+        a_reg[0] = (tid < R && p0 + tid % R < p.k) ? silu_mul(g, u) : 0.0f;
+    }
     if constexpr (NORM) {
 #pragma unroll
         for (int r = 0; r < MM; ++r) {
@@ -415,6 +464,73 @@ int run_skinny_partials(const MatmulArgs& a, const float** partial) {
     *partial = p.direct ? nullptr : p.out;
     return slices;
 }
+
+// x (k = hidden) = silu_mul of a Summed w13 product, times W (hidden x n),
+// one row: the forward pass's SwiGLU and w2 product in one GEMV.
+template <class BT>
+int run_skinny_swiglu_partials(const MatmulArgs& a, const Summed& gu, int hidden,
+                               const float** partial) {
+    if (a.m != 1 || gu.slices > kSwiSlices || a.rms_weight) return 0;
+    const BT* B = static_cast<const BT*>(a.B);
+    int E = 1;
+    if (std::is_same<BT, int8_t>::value && a.n % 16 == 0 && aligned(B, 16)) {
+        E = 16;
+    } else if (a.n % 4 == 0 && aligned(B, 4 * sizeof(BT))) {
+        E = 4;
+    }
+    if (E == 1) return 0;
+    // One A value per thread: at most 256 rows of B per workgroup.
+    int L = rows_per_lane(E, a.m, a.n, a.k);
+    while (E * L > kThreads) L /= 2;
+    const int slices = ceil_div(a.k, E * L);
+    const dim3 grid(ceil_div(a.n, kThreads), slices);
+    GemvParams<BT> p{};
+    p.m = 1;
+    p.n = a.n;
+    p.k = a.k;
+    p.B = B;
+    p.scale = a.scale;
+    p.direct = slices == 1;
+    p.accumulate = a.accumulate && p.direct;
+    p.out = p.direct ? a.C : scratch(kPartialFromPartial, static_cast<size_t>(slices) * a.n);
+    p.gu = gu;
+    p.hidden = hidden;
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, a.stream, p); };
+    if constexpr (std::is_same<BT, int8_t>::value) {
+        if (E == 16) {
+            switch (L) {
+                case 4: go(gemv_kernel<BT, 1, 16, 4, false, true>); break;
+                case 8: go(gemv_kernel<BT, 1, 16, 8, false, true>); break;
+                default: go(gemv_kernel<BT, 1, 16, 16, false, true>); break;
+            }
+            *partial = p.direct ? nullptr : p.out;
+            return slices;
+        }
+    }
+    switch (L) {
+        case 4: go(gemv_kernel<BT, 1, 4, 4, false, true>); break;
+        case 8: go(gemv_kernel<BT, 1, 4, 8, false, true>); break;
+        case 16: go(gemv_kernel<BT, 1, 4, 16, false, true>); break;
+        default: go(gemv_kernel<BT, 1, 4, 32, false, true>); break;
+    }
+    *partial = p.direct ? nullptr : p.out;
+    return slices;
+}
+
+template <class BT>
+bool run_skinny_swiglu(const MatmulArgs& a, const Summed& gu, int hidden) {
+    const float* partial = nullptr;
+    const int slices = run_skinny_swiglu_partials<BT>(a, gu, hidden, &partial);
+    if (slices == 0) return false;
+    if (slices > 1)
+        run_reduce_slices(1, a.n, slices, partial,
+                          std::is_same<BT, int8_t>::value ? a.scale : nullptr, a.C,
+                          a.accumulate, a.stream);
+    return true;
+}
+
+template bool run_skinny_swiglu<float>(const MatmulArgs&, const Summed&, int);
+template bool run_skinny_swiglu<int8_t>(const MatmulArgs&, const Summed&, int);
 
 template <class BT>
 void run_skinny(const MatmulArgs& a) {

@@ -10,6 +10,8 @@
 #include <stdexcept>
 #include <string>
 
+#include "common.hpp"
+
 namespace em {
 
 // A HIP runtime failure; api.hip turns it into EM_EDEVICE with this text.
@@ -25,8 +27,11 @@ inline void hip_check(hipError_t err, const char* what) {
 // Library-owned, grow-only device scratch (split-K partials, the normed copy
 // of A, quantiser column maxima). Growing waits for the device, frees the old
 // buffer and bumps scratch_generation(). Slot 0 holds partials, slot 1 the
-// norm buffer, slot 2 quantiser work space, slot 3 the bf16 planes of A.
-enum ScratchSlot { kPartial = 0, kNorm = 1, kQuant = 2, kSplitA = 3, kSlots = 4 };
+// norm buffer, slot 2 quantiser work space, slot 3 the bf16 planes of A,
+// slot 4 the partials of a GEMV whose A is formed from slot 0's partials
+// (run_skinny_swiglu), which it must not overwrite while reading them.
+enum ScratchSlot { kPartial = 0, kNorm = 1, kQuant = 2, kSplitA = 3, kPartialFromPartial = 4,
+                   kSlots = 5 };
 float* scratch(ScratchSlot slot, std::size_t floats);
 std::size_t scratch_generation();
 
@@ -54,6 +59,12 @@ void run_skinny(const MatmulArgs& a);
 // reduce_slices does (a consumer kernel that fuses the sum).
 template <class BT>
 int run_skinny_partials(const MatmulArgs& a, const float** partial);
+// One row of silu_mul(gate, up) x B, the gate | up product (split at
+// `hidden` = k) given as a Summed with at most 16 slices: the forward pass's
+// SwiGLU formed inside the GEMV's A staging, C (+)= as run_skinny writes
+// it. False (nothing launched) for a shape it does not take.
+template <class BT>
+bool run_skinny_swiglu(const MatmulArgs& a, const Summed& gu, int hidden);
 
 // MFMA over 16/32/64-row tiles with B streamed once and k split across
 // blocks (GpuKernel::tiled_split). A must already be normed.

@@ -37,25 +37,6 @@
 namespace em {
 namespace {
 
-// A product's output as its consumer reads it: C itself (one k slice, or a
-// kernel that writes C), or the skinny GEMV's partials [slice][m][n] summed
-// in slice order and scaled by the column scale: reduce_slices' arithmetic.
-struct Summed {
-    const float* c;
-    const float* partial;
-    const float* scale;  // int8 column scales, null for fp32
-    int slices, n;
-    std::size_t mn;
-};
-
-__device__ __forceinline__ float summed(const Summed& s, int row, int col) {
-    const std::size_t idx = static_cast<std::size_t>(row) * s.n + col;
-    if (s.slices == 1) return s.c[idx];
-    float t = ordered_sum(s.partial + idx, s.mn, s.slices);
-    if (s.scale) t *= s.scale[col];
-    return t;
-}
-
 // x[i] = table[feed[1 + i]], one workgroup per row (the reference's embed,
 // cuda_model.cu:26-31). Token ids were range-checked on the host.
 __global__ __launch_bounds__(kThreads) void embed_kernel(int dim, const int* feed,
@@ -112,8 +93,7 @@ __global__ __launch_bounds__(kThreads) void swiglu_kernel(int rows, int hidden, 
     for (int idx = blockIdx.x * kThreads + threadIdx.x; idx < total;
          idx += gridDim.x * kThreads) {
         const int r = idx / hidden, c = idx % hidden;
-        const float g = summed(src, r, c);
-        hb[idx] = g / (1.0f + expf(-g)) * summed(src, r, hidden + c);
+        hb[idx] = silu_mul(summed(src, r, c), summed(src, r, hidden + c));
     }
 }
 
@@ -211,6 +191,7 @@ private:
     void project(int n, const float* in, const Proj& w, float* out, const float* rms,
                  bool accumulate);
     Summed project_summed(int n, const float* in, const Proj& w, float* out, const float* rms);
+    bool swiglu_w2(const Summed& gu, const Proj& w2);
     void reserve_rows(std::size_t n);
     void enqueue(int n);
     std::size_t buffers_generation() const { return own_generation_ + scratch_generation(); }
@@ -354,6 +335,27 @@ Summed Model::project_summed(int n, const float* in, const Proj& w, float* out,
     return s;
 }
 
+// One decode row: x += silu_mul(gate, up) W2 with the SwiGLU formed inside
+// the w2 GEMV (run_skinny_swiglu) rather than by swiglu_kernel first: one
+// launch fewer, the same values. False if the GEMV does not take the shape.
+bool Model::swiglu_w2(const Summed& gu, const Proj& w2) {
+    MatmulArgs a{};
+    a.m = 1;
+    a.n = w2.cols;
+    a.k = w2.rows;
+    a.A = nullptr;
+    a.B = q8_ ? static_cast<const void*>(w2.q8.p) : static_cast<const void*>(w2.f32.p);
+    a.scale = q8_ ? w2.scale.p : nullptr;
+    a.C = x_.p;
+    a.accumulate = true;
+    a.rms_weight = nullptr;
+    a.stream = stream_;
+    const bool done = q8_ ? run_skinny_swiglu<int8_t>(a, gu, w2.rows)
+                          : run_skinny_swiglu<float>(a, gu, w2.rows);
+    if (done) check(hipGetLastError(), "launch");
+    return done;
+}
+
 void Model::reserve_rows(std::size_t n) {
     if (n <= rows_) return;
     check(hipStreamSynchronize(stream_), "synchronize before growth");
@@ -389,9 +391,11 @@ void Model::enqueue(int n) {
                       attn_scratch_.p, kAttnAutomatic, stream_);
         project(n, att_.p, L.wo, x_.p, nullptr, true);
         const Summed gu = project_summed(n, x_.p, L.w13, gu_.p, L.rms_ffn.p);
-        hipLaunchKernelGGL(swiglu_kernel, dim3(swiglu_blocks), dim3(kThreads), 0, stream_, n, H,
-                           gu, hb_.p);
-        project(n, hb_.p, L.w2, x_.p, nullptr, true);
+        if (!(n == 1 && swiglu_w2(gu, L.w2))) {
+            hipLaunchKernelGGL(swiglu_kernel, dim3(swiglu_blocks), dim3(kThreads), 0, stream_, n,
+                               H, gu, hb_.p);
+            project(n, hb_.p, L.w2, x_.p, nullptr, true);
+        }
     }
     // Only the last row's logits are returned.
     project(1, x_.p + static_cast<std::size_t>(n - 1) * D, wcls_, logits_dev_.p, rms_final_.p,
