@@ -338,10 +338,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
 }
 
 // Deepest rows-per-lane that fits the register file without spilling: with
-// 16 int8 columns per lane, more than one row of A holds 32+ accumulators
-// and 16 loads in flight would pass 256 VGPRs. One row of A leaves room for
-// 32 loads in flight (128 VGPRs).
-constexpr int max_depth(int E, int MM) { return MM == 1 ? 32 : (E == 16 ? 8 : 16); }
+// 16 int8 columns per lane, eight rows of A hold 128 accumulators and 16
+// loads in flight would pass 256 VGPRs (four rows: 155). One row of A leaves
+// room for 32 loads in flight (128 VGPRs).
+constexpr int max_depth(int E, int MM) { return MM == 1 ? 32 : (E == 16 ? (MM <= 4 ? 16 : 8) : 16); }
 
 template <class BT, int MM, int E, int L, bool NORM>
 void launch(const GemvParams<BT>& p, dim3 grid, hipStream_t s) {
@@ -415,8 +415,13 @@ int rows_per_lane(int E, int m, int n, int k) {
         // since a handful of workgroups cannot keep enough loads in flight.
         while (E * L < k) L *= 2;
     } else {
+        // Half a workgroup per CU. Two to four rows of int8 (each lane also
+        // holds 2-4x the accumulators; 16-deep only since four rows fit in
+        // 155 registers): 1.5 per CU, which took m = 4 x 4096x11008 from
+        // 18.5 to 16.4 us and leaves 4096^2 (1 per CU at depth 16) at 8.
         const long long tiles = ceil_div(n, kThreads);
-        const long long target = cu_count() / 2;
+        const bool few_rows = E == 16 && (mm == 2 || mm == 4);
+        const long long target = few_rows ? cu_count() + cu_count() / 2 : cu_count() / 2;
         for (int depth : {16, 8}) {
             if (tiles * ceil_div(k, static_cast<long long>(E) * depth) >= target) {
                 L = depth;
