@@ -308,25 +308,40 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
     if (n == 1) return;  // written by the split kernel
     const std::size_t b = (static_cast<std::size_t>(i) * a.n_heads + h) * a.splits;
     const int tid = threadIdx.x;
-    float mloc = -INFINITY;
-    for (int c = tid; c < n; c += kThreads) mloc = fmaxf(mloc, a.part_ml[b + c].x);
-    const float M = block_max(mloc, part);
-
     const int hs4 = a.head_size / 4;
     const int slots = kThreads / hs4, r = tid / hs4, d = tid % hs4;
     const floatx4* po = reinterpret_cast<const floatx4*>(a.part_o);
     float* red_l = reinterpret_cast<float*>(red4 + slots * hs4);
-    if (r < slots) {
+    const bool worker = r < slots;
+
+    // The first eight splits' (max, sum) and outputs are loaded before the
+    // block max is formed: they do not depend on it, so the merge waits on
+    // one memory latency instead of two.
+    float2 ml[8];
+    floatx4 o[8];
+    if (worker) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int c = min(r + u * slots, n - 1);
+            ml[u] = a.part_ml[b + c];
+            o[u] = po[(b + c) * hs4 + d];
+        }
+    }
+    float mloc = -INFINITY;
+    for (int c = tid; c < n; c += kThreads) mloc = fmaxf(mloc, a.part_ml[b + c].x);
+    const float M = block_max(mloc, part);
+
+    if (worker) {
         floatx4 acc{0.f, 0.f, 0.f, 0.f};
         float l = 0.0f;
         for (int c0 = r; c0 < n; c0 += 8 * slots) {
-            float2 ml[8];
-            floatx4 o[8];
+            if (c0 != r) {
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int c = min(c0 + u * slots, n - 1);
-                ml[u] = a.part_ml[b + c];
-                o[u] = po[(b + c) * hs4 + d];
+                for (int u = 0; u < 8; ++u) {
+                    const int c = min(c0 + u * slots, n - 1);
+                    ml[u] = a.part_ml[b + c];
+                    o[u] = po[(b + c) * hs4 + d];
+                }
             }
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
@@ -342,14 +357,15 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
     }
     __syncthreads();
     if (tid < hs4) {
-        floatx4 o = red4[tid];
+        floatx4 total = red4[tid];
         float l = red_l[0];
         for (int rr = 1; rr < slots; ++rr) {
-            o += red4[rr * hs4 + tid];
+            total += red4[rr * hs4 + tid];
             l += red_l[rr];
         }
         reinterpret_cast<floatx4*>(a.out + static_cast<std::size_t>(i) * a.out_stride +
-                                   static_cast<std::size_t>(h) * a.head_size)[tid] = o * (1.0f / l);
+                                   static_cast<std::size_t>(h) * a.head_size)[tid] =
+            total * (1.0f / l);
     }
 }
 

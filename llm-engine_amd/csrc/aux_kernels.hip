@@ -47,15 +47,21 @@ __global__ __launch_bounds__(kThreads) void naive_kernel(int m, int n, int k, co
     *c = accumulate ? *c + acc : acc;
 }
 
-__global__ __launch_bounds__(kThreads) void reduce_slices_kernel(int mn, int n, int slices,
-                                                                 const float* partial,
-                                                                 const float* scale, float* C,
-                                                                 int accumulate) {
-    const int i = blockIdx.x * kThreads + threadIdx.x;
+// One output per thread in 64-thread workgroups, so that the 4096 outputs
+// of a decode GEMV spread over 64 CUs' load queues rather than 16. C and the
+// scale are loaded before the partials: the one round trip covers all three.
+constexpr int kReduceThreads = 64;
+
+__global__ __launch_bounds__(kReduceThreads) void reduce_slices_kernel(
+    int mn, int n, int slices, const float* __restrict__ partial, const float* __restrict__ scale,
+    float* __restrict__ C, int accumulate) {
+    const int i = blockIdx.x * kReduceThreads + threadIdx.x;
     if (i >= mn) return;
-    float total = ordered_sum(partial + i, static_cast<size_t>(mn), slices);
-    if (scale) total *= scale[i % n];
-    C[i] = accumulate ? C[i] + total : total;
+    const float prior = accumulate ? C[i] : 0.0f;
+    const float sc = scale ? scale[i % n] : 1.0f;
+    float total = ordered_sum(partial, static_cast<uint32_t>(i), static_cast<uint32_t>(mn), slices);
+    if (scale) total *= sc;
+    C[i] = accumulate ? prior + total : total;
 }
 
 // Eight nontemporal 16-byte loads in flight per thread per step, folded
@@ -227,8 +233,9 @@ template void run_naive<int8_t>(const MatmulArgs&);
 void run_reduce_slices(int m, int n, int slices, const float* partial, const float* scale,
                        float* C, bool accumulate, hipStream_t stream) {
     const int mn = m * n;
-    hipLaunchKernelGGL(reduce_slices_kernel, dim3(ceil_div(mn, kThreads)), dim3(kThreads), 0,
-                       stream, mn, n, slices, partial, scale, C, accumulate ? 1 : 0);
+    hipLaunchKernelGGL(reduce_slices_kernel, dim3(ceil_div(mn, kReduceThreads)),
+                       dim3(kReduceThreads), 0, stream, mn, n, slices, partial, scale, C,
+                       accumulate ? 1 : 0);
 }
 
 void run_stream_read(const void* buf, std::size_t bytes, uint32_t* sink, hipStream_t stream) {

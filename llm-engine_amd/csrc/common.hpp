@@ -82,21 +82,40 @@ __device__ __forceinline__ void widen4(uint32_t w, float* out) {
     out[3] = static_cast<float>(static_cast<int8_t>(w >> 24));
 }
 
-// p[0] + p[stride] + ... + p[(slices - 1) * stride], added in slice order
-// (so every caller gets the same bits), with the loads issued 16 at a time
-// so the sum waits on one memory latency per 16 slices, not per slice.
-// (32 at a time measured slower: more registers and padding loads.)
-__device__ __forceinline__ float ordered_sum(const float* p, size_t stride, int slices) {
+// base[idx] + base[idx + stride] + ... (slices terms), added in slice order
+// from +0 (so every caller gets the same bits). The last (or only) 64 slices
+// are loaded before their first add, so the sum waits on one memory latency
+// for up to 64 slices (a GEMV over k = 11008 leaves 43). Those loads are
+// guarded by the slice count (uniform across the wave), never padded; the
+// registers of the slices past it hold +0, and adding +0 leaves a sum that
+// started at +0 unchanged (such a sum is never -0), so the adds need no
+// guard. Offsets are 32-bit byte offsets from a uniform base: a partials
+// buffer holds at most 2^29 floats (slices <= k / 64 + 1 and k * n < 2^31).
+__device__ __forceinline__ float ordered_sum(const float* __restrict__ base, uint32_t idx,
+                                             uint32_t stride, int slices) {
+    const char* bytes = reinterpret_cast<const char*>(base);
+    auto at = [&](uint32_t element) {
+        return *reinterpret_cast<const float*>(bytes + element * 4u);
+    };
     float total = 0.0f;
     int s = 0;
-    for (; s + 16 <= slices; s += 16) {
+    for (; slices - s > 64; s += 16) {
         float v[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = p[static_cast<size_t>(s + i) * stride];
+        for (int i = 0; i < 16; ++i) v[i] = at(idx + static_cast<uint32_t>(s + i) * stride);
 #pragma unroll
         for (int i = 0; i < 16; ++i) total += v[i];
     }
-    for (; s < slices; ++s) total += p[static_cast<size_t>(s) * stride];
+    const int left = slices - s;
+    const uint32_t first = idx + static_cast<uint32_t>(s) * stride;
+    float v[64];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) v[i] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 64; ++i)
+        if (i < left) v[i] = at(first + static_cast<uint32_t>(i) * stride);
+#pragma unroll
+    for (int i = 0; i < 64; ++i) total += v[i];
     return total;
 }
 
@@ -114,7 +133,8 @@ struct Summed {
 __device__ __forceinline__ float summed(const Summed& s, int row, int col) {
     const size_t idx = static_cast<size_t>(row) * s.n + col;
     if (s.slices == 1) return s.c[idx];
-    float t = ordered_sum(s.partial + idx, s.mn, s.slices);
+    float t = ordered_sum(s.partial, static_cast<uint32_t>(idx), static_cast<uint32_t>(s.mn),
+                          s.slices);
     if (s.scale) t *= s.scale[col];
     return t;
 }

@@ -37,13 +37,22 @@
 namespace em {
 namespace {
 
-// x[i] = table[feed[1 + i]], one workgroup per row (the reference's embed,
-// cuda_model.cu:26-31). Token ids were range-checked on the host.
-__global__ __launch_bounds__(kThreads) void embed_kernel(int dim, const int* feed,
-                                                         const float* table, float* x) {
-    const float* src = table + static_cast<std::size_t>(feed[1 + blockIdx.x]) * dim;
-    float* dst = x + static_cast<std::size_t>(blockIdx.x) * dim;
-    for (int j = threadIdx.x; j < dim; j += kThreads) dst[j] = src[j];
+// x[i] = table[feed[1 + i]] (the reference's embed, cuda_model.cu:26-31),
+// row blockIdx.y. One float4 per thread when rows are 16-byte multiples, so
+// a 4096-wide row is four workgroups with one load each; the restrict lets
+// every load issue before the stores. Token ids were range-checked on the host.
+__global__ __launch_bounds__(kThreads) void embed_kernel(int dim, const int* __restrict__ feed,
+                                                         const float* __restrict__ table,
+                                                         float* __restrict__ x) {
+    const std::size_t src = static_cast<std::size_t>(feed[1 + blockIdx.y]) * dim;
+    const std::size_t dst = static_cast<std::size_t>(blockIdx.y) * dim;
+    const int j = blockIdx.x * kThreads + threadIdx.x;
+    if (dim % 4 == 0) {
+        if (j < dim / 4)
+            reinterpret_cast<float4*>(x + dst)[j] = reinterpret_cast<const float4*>(table + src)[j];
+    } else {
+        for (int c = j; c < dim; c += gridDim.x * kThreads) x[dst + c] = table[src + c];
+    }
 }
 
 // Row blockIdx.y, at position feed[0] + blockIdx.y: rotates each (even, odd)
@@ -378,8 +387,8 @@ void Model::enqueue(int n) {
     check(hipMemcpyAsync(feed_dev_.p, feed_host_.p, (n + 1) * sizeof(int), hipMemcpyHostToDevice,
                          stream_),
           "upload feed");
-    hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(kThreads), 0, stream_, D, feed_dev_.p, emb_.p,
-                       x_.p);
+    hipLaunchKernelGGL(embed_kernel, dim3(ceil_div(ceil_div(D, 4), kThreads), n), dim3(kThreads), 0,
+                       stream_, D, feed_dev_.p, emb_.p, x_.p);
     const int rope_threads = D / 2 + KV / 2 + KV;
     const int swiglu_blocks = std::min(ceil_div(static_cast<long long>(n) * H, kThreads), 4096);
     for (LayerDev& L : layers_) {
