@@ -47,21 +47,29 @@ __global__ __launch_bounds__(kThreads) void naive_kernel(int m, int n, int k, co
     *c = accumulate ? *c + acc : acc;
 }
 
-// One output per thread in 64-thread workgroups, so that the 4096 outputs
-// of a decode GEMV spread over 64 CUs' load queues rather than 16. C and the
-// scale are loaded before the partials: the one round trip covers all three.
-constexpr int kReduceThreads = 64;
+// One output per thread. C and the scale are loaded with the first
+// partials, so no round trip waits on them alone. With ssq,
+// each wave (outputs 64w .. 64w + 63, one row of C when n is a multiple of
+// 64) also writes the sum of their squares, by a fixed butterfly.
+// 256-thread workgroups: 64-thread ones measured 0.5 us slower per call.
+static_assert(kSsqChunk == kWave, "one sum of squares per wave");
 
-__global__ __launch_bounds__(kReduceThreads) void reduce_slices_kernel(
+__global__ __launch_bounds__(kThreads) void reduce_slices_kernel(
     int mn, int n, int slices, const float* __restrict__ partial, const float* __restrict__ scale,
-    float* __restrict__ C, int accumulate) {
-    const int i = blockIdx.x * kReduceThreads + threadIdx.x;
-    if (i >= mn) return;
-    const float prior = accumulate ? C[i] : 0.0f;
-    const float sc = scale ? scale[i % n] : 1.0f;
-    float total = ordered_sum(partial, static_cast<uint32_t>(i), static_cast<uint32_t>(mn), slices);
+    float* __restrict__ C, int accumulate, float* __restrict__ ssq) {
+    const int i = blockIdx.x * kThreads + threadIdx.x;
+    const bool in = i < mn;
+    const int ii = in ? i : mn - 1;
+    const float prior = accumulate ? C[ii] : 0.0f;
+    const float sc = scale ? scale[ii % n] : 1.0f;
+    float total = ordered_sum(partial, static_cast<uint32_t>(ii), static_cast<uint32_t>(mn), slices);
     if (scale) total *= sc;
-    C[i] = accumulate ? prior + total : total;
+    const float out = accumulate ? prior + total : total;
+    if (in) C[i] = out;
+    if (ssq) {
+        const float sq = wave_sum(in ? out * out : 0.0f);
+        if (in && threadIdx.x % kWave == 0) ssq[i / kSsqChunk] = sq;
+    }
 }
 
 // Eight nontemporal 16-byte loads in flight per thread per step, folded
@@ -231,11 +239,11 @@ template void run_naive<float>(const MatmulArgs&);
 template void run_naive<int8_t>(const MatmulArgs&);
 
 void run_reduce_slices(int m, int n, int slices, const float* partial, const float* scale,
-                       float* C, bool accumulate, hipStream_t stream) {
+                       float* C, bool accumulate, hipStream_t stream, float* ssq) {
     const int mn = m * n;
-    hipLaunchKernelGGL(reduce_slices_kernel, dim3(ceil_div(mn, kReduceThreads)),
-                       dim3(kReduceThreads), 0, stream, mn, n, slices, partial, scale, C,
-                       accumulate ? 1 : 0);
+    hipLaunchKernelGGL(reduce_slices_kernel, dim3(ceil_div(mn, kThreads)), dim3(kThreads), 0,
+                       stream, mn, n, slices, partial, scale, C, accumulate ? 1 : 0,
+                       n % kSsqChunk == 0 ? ssq : nullptr);
 }
 
 void run_stream_read(const void* buf, std::size_t bytes, uint32_t* sink, hipStream_t stream) {

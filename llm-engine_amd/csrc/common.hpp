@@ -83,39 +83,38 @@ __device__ __forceinline__ void widen4(uint32_t w, float* out) {
 }
 
 // base[idx] + base[idx + stride] + ... (slices terms), added in slice order
-// from +0 (so every caller gets the same bits). The last (or only) 64 slices
-// are loaded before their first add, so the sum waits on one memory latency
-// for up to 64 slices (a GEMV over k = 11008 leaves 43). Those loads are
-// guarded by the slice count (uniform across the wave), never padded; the
-// registers of the slices past it hold +0, and adding +0 leaves a sum that
-// started at +0 unchanged (such a sum is never -0), so the adds need no
-// guard. Offsets are 32-bit byte offsets from a uniform base: a partials
-// buffer holds at most 2^29 floats (slices <= k / 64 + 1 and k * n < 2^31).
+// from +0 (so every caller gets the same bits), with the loads issued 16 at
+// a time so the sum waits on one memory latency per 16 slices. The last
+// partial batch is one more batch of 16 with its loads guarded by the slice
+// count (uniform across the wave) and +0 in the registers past it: adding
+// +0 leaves a sum that started at +0 unchanged (such a sum is never -0). A
+// tail of single load-then-add steps took 11 round trips for a GEMV over
+// k = 11008 (43 slices). The code stays small on purpose: the kernels that
+// call it wait on little else, and one batch of up to 64 measured slower at
+// 32 and 64 slices than two or four of 16.
 __device__ __forceinline__ float ordered_sum(const float* __restrict__ base, uint32_t idx,
                                              uint32_t stride, int slices) {
-    const char* bytes = reinterpret_cast<const char*>(base);
-    auto at = [&](uint32_t element) {
-        return *reinterpret_cast<const float*>(bytes + element * 4u);
-    };
+    const float* p = base + idx;
     float total = 0.0f;
     int s = 0;
-    for (; slices - s > 64; s += 16) {
+    for (; s + 16 <= slices; s += 16) {
         float v[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = at(idx + static_cast<uint32_t>(s + i) * stride);
+        for (int i = 0; i < 16; ++i) v[i] = p[static_cast<size_t>(s + i) * stride];
 #pragma unroll
         for (int i = 0; i < 16; ++i) total += v[i];
     }
-    const int left = slices - s;
-    const uint32_t first = idx + static_cast<uint32_t>(s) * stride;
-    float v[64];
+    if (s < slices) {
+        const int left = slices - s;
+        float v[16];
 #pragma unroll
-    for (int i = 0; i < 64; ++i) v[i] = 0.0f;
+        for (int i = 0; i < 16; ++i) v[i] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 64; ++i)
-        if (i < left) v[i] = at(first + static_cast<uint32_t>(i) * stride);
+        for (int i = 0; i < 16; ++i)
+            if (i < left) v[i] = p[static_cast<size_t>(s + i) * stride];
 #pragma unroll
-    for (int i = 0; i < 64; ++i) total += v[i];
+        for (int i = 0; i < 16; ++i) total += v[i];
+    }
     return total;
 }
 

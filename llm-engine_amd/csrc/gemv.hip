@@ -108,18 +108,27 @@ struct GemvParams {
     int a_vec4;          // k % 4 == 0 and A 16-byte aligned: the norm reads float4
     Summed gu;           // SWI: the w13 product A is formed from
     int hidden;          // SWI: its gate | up split
+    const float* ssq;    // NORM 2: sums of squares of A, one per 64 values
+    int ssq_parts;       // NORM 2: their count, ceil(k / 64) <= kSsqParts
 };
 
 // Slices a SwiGLU source may have: its values are loaded into registers.
 constexpr int kSwiSlices = 16;
+// Sums of squares a NORM 2 row may have: four per lane of one wave.
+constexpr int kSsqParts = 4 * kWave;
 
 // MM: rows of A the kernel is compiled for (m <= MM; extra rows are zero).
-// E: columns per lane. L: rows per lane. NORM: fused RMSNorm of A.
+// E: columns per lane. L: rows per lane. NORM: fused RMSNorm of A, 0 none,
+// 1 with the sum of squares formed here over all of A's row, 2 (one row)
+// with it formed from the sums of squares the producer of A left, one per
+// 64 values (p.ssq): each wave adds them with a fixed butterfly, so every
+// lane and workgroup gets the same bits without a barrier, and no
+// workgroup reads more of A than its own slice.
 // SWI (one row, at most 256 rows of k per workgroup): A is not read but
 // formed, A[j] = silu_mul(gate[j], up[j]) of a product given as a Summed
 // (p.gu, gate | up at p.hidden): the arithmetic of the forward pass's SwiGLU
 // kernel, so the result is the same as running that kernel first.
-template <class BT, int MM, int E, int L, bool NORM, bool SWI = false>
+template <class BT, int MM, int E, int L, int NORM, bool SWI = false>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
     using LT = Lane<BT, E>;
     using V = typename LT::V;
@@ -145,14 +154,15 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
     // of (k = tid, tid + 256, ...), loaded before the weight loads. A loop
     // of loads after them would wait for the whole weight stream at its
     // first s_waitcnt and then take one L2 round trip per step.
-    constexpr int NP = !NORM ? 1 : MM == 1 ? 32 : MM == 2 ? 16 : MM <= 4 ? 4 : 2;
+    static_assert(NORM != 2 || (MM == 1 && !SWI), "producer sums of squares: one row");
+    constexpr int NP = NORM != 1 ? 1 : MM == 1 ? 32 : MM == 2 ? 16 : MM <= 4 ? 4 : 2;
     // Loads are unconditional (addresses clamped into A; k >= 1 here) so
     // that no branch separates them; values past m or k are masked at use.
     // With a_vec4 the thread takes float4 f = tid, tid + 256, ... (values
     // 4f .. 4f + 3): a quarter of the load instructions.
     constexpr int NP4 = NP / 4;
     float npre[MM][NP];
-    if constexpr (NORM) {
+    if constexpr (NORM == 1) {
 #pragma unroll
         for (int r = 0; r < MM; ++r) {
             const int rr = r < p.m ? r : p.m - 1;
@@ -202,6 +212,19 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
             a_reg[t] = (idx < MM * R && r < p.m && pp < p.k) ? p.A[r * p.k + pp] : 0.0f;
         }
     }
+    // NORM 2: this lane's share of the sums of squares (parts lane, lane +
+    // 64, ...) and the norm weights of its slice values, before the weights.
+    float sq[NORM == 2 ? kSsqParts / kWave : 1];
+    float gain[NORM == 2 ? AREG : 1];
+    if constexpr (NORM == 2) {
+        const int lane = tid % kWave;
+#pragma unroll
+        for (int j = 0; j < kSsqParts / kWave; ++j)
+            sq[j] = p.ssq[min(lane + j * kWave, p.ssq_parts - 1)];
+#pragma unroll
+        for (int t = 0; t < AREG; ++t)
+            gain[t] = p.rms_weight[min(p0 + (tid + t * kThreads) % R, p.k - 1)];
+    }
 
     // All L weight vectors of this lane in flight at once. No load is
     // predicated and no loaded value is selected, so nothing sits between a
@@ -239,7 +262,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
         }
         a_reg[0] = (tid < R && p0 + tid % R < p.k) ? silu_mul(g, u) : 0.0f;
     }
-    if constexpr (NORM) {
+    if constexpr (NORM == 1) {
 #pragma unroll
         for (int r = 0; r < MM; ++r) {
             // One fixed sequence of fmaf per thread: the preloaded values
@@ -276,14 +299,26 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
         }
         __syncthreads();
     }
+    float rs2 = 0.0f;
+    if constexpr (NORM == 2) {
+        // Parts past ssq_parts add +0: a sum of squares is never -0.
+        const int lane = tid % kWave;
+        float v = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kSsqParts / kWave; ++j)
+            v += lane + j * kWave < p.ssq_parts ? sq[j] : 0.0f;
+        rs2 = 1.0f / sqrtf(wave_sum(v) / static_cast<float>(p.k) + kRmsEps);
+    }
 #pragma unroll
     for (int t = 0; t < AREG; ++t) {
         const int idx = tid + t * kThreads;
         if (idx < MM * R) {
             float v = a_reg[t];
-            if constexpr (NORM) {
+            if constexpr (NORM == 1) {
                 const int r = idx / R, pp = p0 + idx % R;
                 if (r < p.m && pp < p.k) v = v * rs_s[r] * p.rms_weight[pp];
+            } else if constexpr (NORM == 2) {
+                if (p0 + idx % R < p.k) v = v * rs2 * gain[t];
             }
             a_s[idx] = v;
         }
@@ -343,14 +378,16 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
 // room for 32 loads in flight (128 VGPRs).
 constexpr int max_depth(int E, int MM) { return MM == 1 ? 32 : (E == 16 ? (MM <= 4 ? 16 : 8) : 16); }
 
-template <class BT, int MM, int E, int L, bool NORM>
+template <class BT, int MM, int E, int L, int NORM>
 void launch(const GemvParams<BT>& p, dim3 grid, hipStream_t s) {
     hipLaunchKernelGGL((gemv_kernel<BT, MM, E, L, NORM>), grid, dim3(kThreads), 0, s, p);
 }
 
-template <class BT, int E, int L, bool NORM>
+template <class BT, int E, int L, int NORM>
 void pick_rows(const GemvParams<BT>& p, dim3 grid, hipStream_t s) {
-    if (p.m <= 1) {
+    if constexpr (NORM == 2) {
+        launch<BT, 1, E, L, 2>(p, grid, s);  // one row (run_skinny_partials checks)
+    } else if (p.m <= 1) {
         launch<BT, 1, E, L, NORM>(p, grid, s);
     } else if (p.m <= 2) {
         launch<BT, 2, E, (L < max_depth(E, 2) ? L : max_depth(E, 2)), NORM>(p, grid, s);
@@ -361,7 +398,7 @@ void pick_rows(const GemvParams<BT>& p, dim3 grid, hipStream_t s) {
     }
 }
 
-template <class BT, int E, bool NORM>
+template <class BT, int E, int NORM>
 void pick_depth(int L, const GemvParams<BT>& p, dim3 grid, hipStream_t s) {
     if constexpr (E == 1) {
         pick_rows<BT, 1, 16, NORM>(p, grid, s);
@@ -375,7 +412,7 @@ void pick_depth(int L, const GemvParams<BT>& p, dim3 grid, hipStream_t s) {
     }
 }
 
-template <class BT, bool NORM>
+template <class BT, int NORM>
 void pick_width(int E, int L, const GemvParams<BT>& p, dim3 grid, hipStream_t s) {
     if constexpr (std::is_same<BT, int8_t>::value) {
         if (E == 16) return pick_depth<BT, 16, NORM>(L, p, grid, s);
@@ -461,10 +498,14 @@ int run_skinny_partials(const MatmulArgs& a, const float** partial) {
     p.accumulate = a.accumulate && p.direct;
     p.out = p.direct ? a.C
                      : scratch(kPartial, static_cast<size_t>(slices) * a.m * a.n);
-    if (a.rms_weight) {
-        pick_width<BT, true>(E, L, p, grid, a.stream);
+    p.ssq = a.ssq;
+    p.ssq_parts = ceil_div(a.k, kSsqChunk);
+    if (a.rms_weight && a.ssq && a.m == 1 && p.ssq_parts <= kSsqParts) {
+        pick_width<BT, 2>(E, L, p, grid, a.stream);
+    } else if (a.rms_weight) {
+        pick_width<BT, 1>(E, L, p, grid, a.stream);
     } else {
-        pick_width<BT, false>(E, L, p, grid, a.stream);
+        pick_width<BT, 0>(E, L, p, grid, a.stream);
     }
     *partial = p.direct ? nullptr : p.out;
     return slices;
@@ -504,38 +545,37 @@ int run_skinny_swiglu_partials(const MatmulArgs& a, const Summed& gu, int hidden
     if constexpr (std::is_same<BT, int8_t>::value) {
         if (E == 16) {
             switch (L) {
-                case 4: go(gemv_kernel<BT, 1, 16, 4, false, true>); break;
-                case 8: go(gemv_kernel<BT, 1, 16, 8, false, true>); break;
-                default: go(gemv_kernel<BT, 1, 16, 16, false, true>); break;
+                case 4: go(gemv_kernel<BT, 1, 16, 4, 0, true>); break;
+                case 8: go(gemv_kernel<BT, 1, 16, 8, 0, true>); break;
+                default: go(gemv_kernel<BT, 1, 16, 16, 0, true>); break;
             }
             *partial = p.direct ? nullptr : p.out;
             return slices;
         }
     }
     switch (L) {
-        case 4: go(gemv_kernel<BT, 1, 4, 4, false, true>); break;
-        case 8: go(gemv_kernel<BT, 1, 4, 8, false, true>); break;
-        case 16: go(gemv_kernel<BT, 1, 4, 16, false, true>); break;
-        default: go(gemv_kernel<BT, 1, 4, 32, false, true>); break;
+        case 4: go(gemv_kernel<BT, 1, 4, 4, 0, true>); break;
+        case 8: go(gemv_kernel<BT, 1, 4, 8, 0, true>); break;
+        case 16: go(gemv_kernel<BT, 1, 4, 16, 0, true>); break;
+        default: go(gemv_kernel<BT, 1, 4, 32, 0, true>); break;
     }
     *partial = p.direct ? nullptr : p.out;
     return slices;
 }
 
 template <class BT>
-bool run_skinny_swiglu(const MatmulArgs& a, const Summed& gu, int hidden) {
+int run_skinny_swiglu(const MatmulArgs& a, const Summed& gu, int hidden, float* ssq) {
     const float* partial = nullptr;
     const int slices = run_skinny_swiglu_partials<BT>(a, gu, hidden, &partial);
-    if (slices == 0) return false;
     if (slices > 1)
         run_reduce_slices(1, a.n, slices, partial,
                           std::is_same<BT, int8_t>::value ? a.scale : nullptr, a.C,
-                          a.accumulate, a.stream);
-    return true;
+                          a.accumulate, a.stream, ssq);
+    return slices;
 }
 
-template bool run_skinny_swiglu<float>(const MatmulArgs&, const Summed&, int);
-template bool run_skinny_swiglu<int8_t>(const MatmulArgs&, const Summed&, int);
+template int run_skinny_swiglu<float>(const MatmulArgs&, const Summed&, int, float*);
+template int run_skinny_swiglu<int8_t>(const MatmulArgs&, const Summed&, int, float*);
 
 template <class BT>
 void run_skinny(const MatmulArgs& a) {

@@ -38,6 +38,10 @@ std::size_t scratch_generation();
 // Compute units of the current device (cached).
 int cu_count();
 
+// Values per sum of squares that a producer of a GEMV's A may leave for the
+// GEMV's norm (embed and the residual reduce, in the forward pass).
+constexpr int kSsqChunk = 64;
+
 struct MatmulArgs {
     int m, n, k;
     const float* A;
@@ -47,6 +51,10 @@ struct MatmulArgs {
     bool accumulate;
     const float* rms_weight;  // null: no norm
     hipStream_t stream;
+    // With rms_weight and m == 1 (GEMV only): the sums of squares of A's
+    // values [64j, 64j + 64), j < ceil(k / 64), that A's producer left; the
+    // norm is formed from them instead of from all of A in every workgroup.
+    const float* ssq;
 };
 
 // Decode-shaped GEMV, m <= 8 (GpuKernel::skinny). Fuses the norm.
@@ -62,9 +70,11 @@ int run_skinny_partials(const MatmulArgs& a, const float** partial);
 // One row of silu_mul(gate, up) x B, the gate | up product (split at
 // `hidden` = k) given as a Summed with at most 16 slices: the forward pass's
 // SwiGLU formed inside the GEMV's A staging, C (+)= as run_skinny writes
-// it. False (nothing launched) for a shape it does not take.
+// it. Returns its k slices; 0 (nothing launched) for a shape it does not
+// take. With more than one slice the reduce also writes ssq (as
+// run_reduce_slices does) when ssq is given and n % 64 == 0.
 template <class BT>
-bool run_skinny_swiglu(const MatmulArgs& a, const Summed& gu, int hidden);
+int run_skinny_swiglu(const MatmulArgs& a, const Summed& gu, int hidden, float* ssq = nullptr);
 
 // MFMA over 16/32/64-row tiles with B streamed once and k split across
 // blocks (GpuKernel::tiled_split). A must already be normed.
@@ -94,8 +104,10 @@ void run_rmsnorm_rows(int m, int k, const float* A, const float* w, float* out,
                       hipStream_t stream);
 
 // C[i] = (accumulate ? C[i] : 0) + scale[i % n] * sum_s partial[s][i], s in order.
+// With ssq (n % 64 == 0): also ssq[j] = the sum of squares of the new
+// C[64j .. 64j + 63], for a GEMV norm over C's rows (MatmulArgs::ssq).
 void run_reduce_slices(int m, int n, int slices, const float* partial, const float* scale,
-                       float* C, bool accumulate, hipStream_t stream);
+                       float* C, bool accumulate, hipStream_t stream, float* ssq = nullptr);
 
 // Zero `count` floats with a kernel (not hipMemsetAsync, so graph capture is safe).
 void run_fill_zero(float* p, std::size_t count, hipStream_t stream);

@@ -40,16 +40,30 @@ namespace {
 // x[i] = table[feed[1 + i]] (the reference's embed, cuda_model.cu:26-31),
 // row blockIdx.y. One float4 per thread when rows are 16-byte multiples, so
 // a 4096-wide row is four workgroups with one load each; the restrict lets
-// every load issue before the stores. Token ids were range-checked on the host.
+// every load issue before the stores. With ssq (dim % 64 == 0, one row) it
+// also writes the sum of squares of each 64 values, for the first layer's
+// qkv GEMV norm: 16 lanes' float4s, added by a fixed butterfly. Token ids
+// were range-checked on the host.
 __global__ __launch_bounds__(kThreads) void embed_kernel(int dim, const int* __restrict__ feed,
                                                          const float* __restrict__ table,
-                                                         float* __restrict__ x) {
+                                                         float* __restrict__ x,
+                                                         float* __restrict__ ssq) {
     const std::size_t src = static_cast<std::size_t>(feed[1 + blockIdx.y]) * dim;
     const std::size_t dst = static_cast<std::size_t>(blockIdx.y) * dim;
     const int j = blockIdx.x * kThreads + threadIdx.x;
     if (dim % 4 == 0) {
-        if (j < dim / 4)
-            reinterpret_cast<float4*>(x + dst)[j] = reinterpret_cast<const float4*>(table + src)[j];
+        const bool in = j < dim / 4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (in) {
+            v = reinterpret_cast<const float4*>(table + src)[j];
+            reinterpret_cast<float4*>(x + dst)[j] = v;
+        }
+        if (ssq) {
+            float sq = fmaf(v.w, v.w, fmaf(v.z, v.z, fmaf(v.y, v.y, v.x * v.x)));
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) sq += __shfl_xor(sq, o, kWave);
+            if (in && j % 16 == 0) ssq[j / 16] = sq;
+        }
     } else {
         for (int c = j; c < dim; c += gridDim.x * kThreads) x[dst + c] = table[src + c];
     }
@@ -199,8 +213,12 @@ private:
     void make_proj(Proj& p, const float* w, int rows, int cols, Buf<float>& staging);
     void project(int n, const float* in, const Proj& w, float* out, const float* rms,
                  bool accumulate);
-    Summed project_summed(int n, const float* in, const Proj& w, float* out, const float* rms);
-    bool swiglu_w2(const Summed& gu, const Proj& w2);
+    MatmulArgs gemv_args(int n, const float* in, const Proj& w, float* out, const float* rms,
+                         bool accumulate, const float* ssq) const;
+    Summed project_summed(int n, const float* in, const Proj& w, float* out, const float* rms,
+                          const float* ssq);
+    bool residual(int n, const float* in, const Proj& w);
+    bool swiglu_w2(const Summed& gu, const Proj& w2, bool* wrote_ssq);
     void reserve_rows(std::size_t n);
     void enqueue(int n);
     std::size_t buffers_generation() const { return own_generation_ + scratch_generation(); }
@@ -219,6 +237,10 @@ private:
 
     std::size_t rows_ = 0, own_generation_ = 0;
     Buf<float> x_, qkv_, att_, gu_, hb_, attn_scratch_;
+    // One-token steps: sums of squares of x per 64 values, left by the
+    // kernel that last wrote x for the next norm GEMV (dim % 64 == 0).
+    bool use_ssq_ = false;
+    Buf<float> ssq_;
 
     Pinned<int> feed_host_;  // [pos, tokens...]
     Buf<int> feed_dev_;
@@ -271,6 +293,8 @@ Model::Model(const em_model_config& c, const float* emb, const em_layer_weights*
 
     logits_dev_.alloc(V);
     feed_dev_.alloc(c.seq_len + 1);
+    use_ssq_ = D % kSsqChunk == 0 && D / kSsqChunk <= 256;
+    if (use_ssq_) ssq_.alloc(D / kSsqChunk);
     check(hipStreamSynchronize(stream_), "load weights");
     reserve_rows(1);
 }
@@ -313,16 +337,8 @@ void Model::project(int n, const float* in, const Proj& w, float* out, const flo
     if (rc != EM_OK) throw DeviceError(em_last_error());
 }
 
-// out = rmsnorm(in) W for a consumer that reads it through summed(): at
-// decode sizes the skinny GEMV leaves its k-slice partials (no reduce
-// launch), otherwise the product is written to out as project() does.
-Summed Model::project_summed(int n, const float* in, const Proj& w, float* out,
-                             const float* rms) {
-    Summed s{out, nullptr, nullptr, 1, w.cols, static_cast<std::size_t>(n) * w.cols};
-    if (n > 8) {
-        project(n, in, w, out, rms, false);
-        return s;
-    }
+MatmulArgs Model::gemv_args(int n, const float* in, const Proj& w, float* out, const float* rms,
+                            bool accumulate, const float* ssq) const {
     MatmulArgs a{};
     a.m = n;
     a.n = w.cols;
@@ -331,9 +347,25 @@ Summed Model::project_summed(int n, const float* in, const Proj& w, float* out,
     a.B = q8_ ? static_cast<const void*>(w.q8.p) : static_cast<const void*>(w.f32.p);
     a.scale = q8_ ? w.scale.p : nullptr;
     a.C = out;
-    a.accumulate = false;
+    a.accumulate = accumulate;
     a.rms_weight = rms;
     a.stream = stream_;
+    a.ssq = ssq;
+    return a;
+}
+
+// out = rmsnorm(in) W for a consumer that reads it through summed(): at
+// decode sizes the skinny GEMV leaves its k-slice partials (no reduce
+// launch), otherwise the product is written to out as project() does.
+// ssq: the sums of squares of `in` that its producer left (one row), or null.
+Summed Model::project_summed(int n, const float* in, const Proj& w, float* out,
+                             const float* rms, const float* ssq) {
+    Summed s{out, nullptr, nullptr, 1, w.cols, static_cast<std::size_t>(n) * w.cols};
+    if (n > 8) {
+        project(n, in, w, out, rms, false);
+        return s;
+    }
+    const MatmulArgs a = gemv_args(n, in, w, out, rms, false, ssq);
     const float* partial = nullptr;
     s.slices = q8_ ? run_skinny_partials<int8_t>(a, &partial) : run_skinny_partials<float>(a, &partial);
     check(hipGetLastError(), "launch");
@@ -344,25 +376,35 @@ Summed Model::project_summed(int n, const float* in, const Proj& w, float* out,
     return s;
 }
 
+// x += in W. For one row with the sums of squares in use, the GEMV's slice
+// reduce also leaves those of the new x (true); otherwise as project().
+bool Model::residual(int n, const float* in, const Proj& w) {
+    if (n != 1 || !use_ssq_) {
+        project(n, in, w, x_.p, nullptr, true);
+        return false;
+    }
+    const MatmulArgs a = gemv_args(1, in, w, x_.p, nullptr, true, nullptr);
+    const float* partial = nullptr;
+    const int slices =
+        q8_ ? run_skinny_partials<int8_t>(a, &partial) : run_skinny_partials<float>(a, &partial);
+    if (slices > 1)
+        run_reduce_slices(1, w.cols, slices, partial, a.scale, x_.p, true, stream_, ssq_.p);
+    check(hipGetLastError(), "launch");
+    return slices > 1;
+}
+
 // One decode row: x += silu_mul(gate, up) W2 with the SwiGLU formed inside
 // the w2 GEMV (run_skinny_swiglu) rather than by swiglu_kernel first: one
 // launch fewer, the same values. False if the GEMV does not take the shape.
-bool Model::swiglu_w2(const Summed& gu, const Proj& w2) {
-    MatmulArgs a{};
-    a.m = 1;
-    a.n = w2.cols;
-    a.k = w2.rows;
-    a.A = nullptr;
-    a.B = q8_ ? static_cast<const void*>(w2.q8.p) : static_cast<const void*>(w2.f32.p);
-    a.scale = q8_ ? w2.scale.p : nullptr;
-    a.C = x_.p;
-    a.accumulate = true;
-    a.rms_weight = nullptr;
-    a.stream = stream_;
-    const bool done = q8_ ? run_skinny_swiglu<int8_t>(a, gu, w2.rows)
-                          : run_skinny_swiglu<float>(a, gu, w2.rows);
-    if (done) check(hipGetLastError(), "launch");
-    return done;
+// *wrote_ssq: whether the sums of squares of the new x were left.
+bool Model::swiglu_w2(const Summed& gu, const Proj& w2, bool* wrote_ssq) {
+    const MatmulArgs a = gemv_args(1, nullptr, w2, x_.p, nullptr, true, nullptr);
+    float* ssq = use_ssq_ ? ssq_.p : nullptr;
+    const int slices = q8_ ? run_skinny_swiglu<int8_t>(a, gu, w2.rows, ssq)
+                           : run_skinny_swiglu<float>(a, gu, w2.rows, ssq);
+    if (slices) check(hipGetLastError(), "launch");
+    *wrote_ssq = ssq && slices > 1;
+    return slices > 0;
 }
 
 void Model::reserve_rows(std::size_t n) {
@@ -387,28 +429,44 @@ void Model::enqueue(int n) {
     check(hipMemcpyAsync(feed_dev_.p, feed_host_.p, (n + 1) * sizeof(int), hipMemcpyHostToDevice,
                          stream_),
           "upload feed");
+    // One-token steps hand the norm GEMVs the sums of squares of x from
+    // whichever kernel last wrote x (embed, or a residual reduce).
+    bool have_ssq = n == 1 && use_ssq_;
     hipLaunchKernelGGL(embed_kernel, dim3(ceil_div(ceil_div(D, 4), kThreads), n), dim3(kThreads), 0,
-                       stream_, D, feed_dev_.p, emb_.p, x_.p);
+                       stream_, D, feed_dev_.p, emb_.p, x_.p, have_ssq ? ssq_.p : nullptr);
     const int rope_threads = D / 2 + KV / 2 + KV;
     const int swiglu_blocks = std::min(ceil_div(static_cast<long long>(n) * H, kThreads), 4096);
     for (LayerDev& L : layers_) {
-        const Summed qkv = project_summed(n, x_.p, L.wqkv, qkv_.p, L.rms_att.p);
+        const Summed qkv = project_summed(n, x_.p, L.wqkv, qkv_.p, L.rms_att.p,
+                                          have_ssq ? ssq_.p : nullptr);
         hipLaunchKernelGGL(rope_cache_kernel, dim3(ceil_div(rope_threads, kThreads), n),
                            dim3(kThreads), 0, stream_, qkv, qkv_cols, D, KV, hs, feed_dev_.p,
                            rope_cos_.p, rope_sin_.p, qkv_.p, L.kcache.p, L.vcache.p);
         run_attention(shape_, n, feed_dev_.p, qkv_.p, L.kcache.p, L.vcache.p, att_.p,
                       attn_scratch_.p, kAttnAutomatic, stream_);
-        project(n, att_.p, L.wo, x_.p, nullptr, true);
-        const Summed gu = project_summed(n, x_.p, L.w13, gu_.p, L.rms_ffn.p);
-        if (!(n == 1 && swiglu_w2(gu, L.w2))) {
+        have_ssq = residual(n, att_.p, L.wo);
+        const Summed gu = project_summed(n, x_.p, L.w13, gu_.p, L.rms_ffn.p,
+                                         have_ssq ? ssq_.p : nullptr);
+        if (!(n == 1 && swiglu_w2(gu, L.w2, &have_ssq))) {
             hipLaunchKernelGGL(swiglu_kernel, dim3(swiglu_blocks), dim3(kThreads), 0, stream_, n,
                                H, gu, hb_.p);
             project(n, hb_.p, L.w2, x_.p, nullptr, true);
+            have_ssq = false;
         }
     }
     // Only the last row's logits are returned.
-    project(1, x_.p + static_cast<std::size_t>(n - 1) * D, wcls_, logits_dev_.p, rms_final_.p,
-            false);
+    const float* x_last = x_.p + static_cast<std::size_t>(n - 1) * D;
+    if (have_ssq) {
+        const MatmulArgs a =
+            gemv_args(1, x_last, wcls_, logits_dev_.p, rms_final_.p, false, ssq_.p);
+        if (q8_) {
+            run_skinny<int8_t>(a);
+        } else {
+            run_skinny<float>(a);
+        }
+    } else {
+        project(1, x_last, wcls_, logits_dev_.p, rms_final_.p, false);
+    }
     check(hipMemcpyAsync(logits_host_.p, logits_dev_.p, cfg_.vocab_size * sizeof(float),
                          hipMemcpyDeviceToHost, stream_),
           "download logits");
