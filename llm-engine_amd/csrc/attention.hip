@@ -80,10 +80,11 @@ int split_lanes(const AttnShape& s) {
 }
 int split_f(const AttnShape& s) { return (s.head_size / 4 + split_lanes(s) - 1) / split_lanes(s); }
 
-std::size_t split_lds(const AttnShape& s) {
+// Slot merge buffers, plus with RoPE fused the G queries, key and value.
+std::size_t split_lds(const AttnShape& s, bool rope = false) {
     const std::size_t G = heads_per_block(s), hs = s.head_size;
     const std::size_t ns = kThreads / split_lanes(s);
-    return (G * ns * hs + 2 * G * ns) * sizeof(float);
+    return (G * ns * hs + 2 * G * ns + (rope ? (G + 2) * hs : 0)) * sizeof(float);
 }
 
 struct SplitScratch {
@@ -130,6 +131,15 @@ struct AttnArgs {
     float* part_o;
     float2* part_ml;
     float* out;
+    // One-row decode with RoPE fused (attn_split_kernel<..., true>): the qkv
+    // product as its consumers read it (q at column 0, k at dim, v at
+    // dim + kv_dim), the rotation tables, and the caches to write.
+    Summed src;
+    int dim, kv_dim;
+    const float* cos_t;
+    const float* sin_t;
+    float* kc_w;
+    float* vc_w;
 };
 
 // Lanes per key row: hs4 rounded up to a power of two, at most one wave.
@@ -148,7 +158,15 @@ constexpr int kRoundPerSlot = 8;
 // d = sub + f * LPP of it (F per lane). Each slot keeps an online softmax of
 // its positions in registers (running max m, sum l, weighted values o) for
 // the G heads; the NS = 256 / LPP slots are then merged in LDS in slot order.
-template <int G, int LPP, int F>
+//
+// ROPE (one row, the forward pass's decode step): the query is not read
+// from a.q but formed here from the qkv product (a.src): summed, rotated as
+// rope_cache_kernel rotates it (rope_pair), into LDS. The last chunk also
+// forms the current position's key and value, writes them to the caches
+// (the workgroup of the first head group of each kv head) and takes that
+// position in slot 0 after its loop, from LDS: no workgroup reads a cache
+// row written in the same launch.
+template <int G, int LPP, int F, bool ROPE = false>
 __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
     constexpr int NS = kThreads / LPP;
     constexpr int PP = kMinChunk / NS < kRoundPerSlot ? (kMinChunk / NS > 0 ? kMinChunk / NS : 1)
@@ -167,6 +185,46 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
     const int h0 = hg * G;
     const int kv_off = (h0 / a.group) * hs;
     const int tid = threadIdx.x, sub = tid % LPP, slot = tid / LPP;
+    // With ROPE the last position (the current one) is not in the cache yet.
+    const bool own_pos = ROPE && s == nchunks - 1;
+    const int loop_len = own_pos ? len - 1 : len;
+    float* rq = lds + G * NS * hs + 2 * G * NS;  // ROPE: G rotated queries, key, value
+    if constexpr (ROPE) {
+        const int pos = n_ctx - 1, half = hs / 2;
+        const float* cs = a.cos_t + static_cast<std::size_t>(pos) * half;
+        const float* sn = a.sin_t + static_cast<std::size_t>(pos) * half;
+        const bool writer = h0 % a.group == 0;
+        const int nq = G * hs4, total = nq + (own_pos ? 2 * hs4 : 0);
+        for (int j = tid; j < total; j += kThreads) {
+            int col, d;
+            bool rot = true;
+            if (j < nq) {
+                d = j % hs4;
+                col = h0 * hs + 4 * j;
+            } else if (j < nq + hs4) {
+                d = j - nq;
+                col = a.dim + kv_off + 4 * d;
+            } else {
+                d = j - nq - hs4;
+                col = a.dim + a.kv_dim + kv_off + 4 * d;
+                rot = false;
+            }
+            const floatx4 x = summed4(a.src, 0, col);
+            floatx4 y = x;
+            if (rot) {
+                const float2 r0 = rope_pair(x.x, x.y, cs[2 * d], sn[2 * d]);
+                const float2 r1 = rope_pair(x.z, x.w, cs[2 * d + 1], sn[2 * d + 1]);
+                y = floatx4{r0.x, r0.y, r1.x, r1.y};
+            }
+            reinterpret_cast<floatx4*>(rq)[j] = y;
+            if (j >= nq && writer) {
+                float* cache = j < nq + hs4 ? a.kc_w : a.vc_w;
+                reinterpret_cast<floatx4*>(cache + static_cast<std::size_t>(pos) * a.kv_stride +
+                                           kv_off)[d] = y;
+            }
+        }
+        __syncthreads();
+    }
 
     // This lane's columns; lanes past hs4 read the last column with a zero
     // query and store nothing.
@@ -179,7 +237,8 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
         dcol[f] = dok[f] ? d : hs4 - 1;
     }
     floatx4 q[G][F];
-    const float* qrow = a.q + static_cast<std::size_t>(i) * a.q_stride + static_cast<std::size_t>(h0) * hs;
+    const float* qrow = ROPE ? rq : a.q + static_cast<std::size_t>(i) * a.q_stride +
+                                        static_cast<std::size_t>(h0) * hs;
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
@@ -200,13 +259,13 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
 
     const float* kbase = a.kc + static_cast<std::size_t>(t0) * a.kv_stride + kv_off;
     const float* vbase = a.vc + static_cast<std::size_t>(t0) * a.kv_stride + kv_off;
-    for (int b0 = 0; b0 < len; b0 += ROUND) {
+    for (int b0 = 0; b0 < loop_len; b0 += ROUND) {
         // Every key and value of the round in flight; positions past the
         // chunk re-read its last position and are masked below.
         floatx4 kv[PP][F], vv[PP][F];
 #pragma unroll
         for (int pp = 0; pp < PP; ++pp) {
-            const int t = min(b0 + slot + pp * NS, len - 1);
+            const int t = min(b0 + slot + pp * NS, loop_len - 1);
             const floatx4* kr = reinterpret_cast<const floatx4*>(kbase + static_cast<std::size_t>(t) * a.kv_stride);
             const floatx4* vr = reinterpret_cast<const floatx4*>(vbase + static_cast<std::size_t>(t) * a.kv_stride);
 #pragma unroll
@@ -218,7 +277,7 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
         float sc[G][PP];
 #pragma unroll
         for (int pp = 0; pp < PP; ++pp) {
-            const bool valid = b0 + slot + pp * NS < len;
+            const bool valid = b0 + slot + pp * NS < loop_len;
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 float dot = 0.0f;
@@ -250,6 +309,35 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
 #pragma unroll
                 for (int f = 0; f < F; ++f) o[g][f] += e * vv[pp][f];
             }
+            m[g] = mn;
+        }
+    }
+
+    if (own_pos && slot == 0) {
+        // The current position, in slot 0: its key and value from LDS.
+        floatx4 kx[F], vx[F];
+#pragma unroll
+        for (int f = 0; f < F; ++f) {
+            kx[f] = reinterpret_cast<const floatx4*>(rq + G * hs)[dcol[f]];
+            vx[f] = reinterpret_cast<const floatx4*>(rq + G * hs + hs)[dcol[f]];
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float dot = 0.0f;
+#pragma unroll
+            for (int f = 0; f < F; ++f) {
+                const floatx4 x = q[g][f] * kx[f];
+                dot += (x.x + x.y) + (x.z + x.w);
+            }
+#pragma unroll
+            for (int off = LPP / 2; off > 0; off >>= 1) dot += __shfl_xor(dot, off, kWave);
+            const float sc = dot * scale;
+            const float mn = fmaxf(m[g], sc);
+            const float alpha = expf(m[g] - mn);
+            const float e = expf(sc - mn);
+            l[g] = l[g] * alpha + e;
+#pragma unroll
+            for (int f = 0; f < F; ++f) o[g][f] = o[g][f] * alpha + e * vx[f];
             m[g] = mn;
         }
     }
@@ -611,27 +699,30 @@ void launch_tile(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t st
     }
 }
 
-template <int G, int LPP, int F>
+template <int G, int LPP, int F, bool ROPE>
 void launch_split(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t stream) {
     const dim3 grid(s.n_heads / G, rows, a.splits);
-    hipLaunchKernelGGL((attn_split_kernel<G, LPP, F>), grid, dim3(kThreads), split_lds(s), stream, a);
+    hipLaunchKernelGGL((attn_split_kernel<G, LPP, F, ROPE>), grid, dim3(kThreads),
+                       split_lds(s, ROPE), stream, a);
     if (a.splits == 1) return;  // one chunk per row: written directly
     const std::size_t hs4 = s.head_size / 4, slots = kThreads / hs4;
     hipLaunchKernelGGL(attn_merge_kernel, dim3(s.n_heads, rows), dim3(kThreads),
                        (slots * hs4 * 4 + slots) * sizeof(float), stream, a);
 }
 
-template <int G>
+template <int G, bool ROPE = false>
 void launch_split_g(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t stream) {
     switch (split_lanes(s) * 10 + split_f(s)) {
-        case 41: launch_split<G, 4, 1>(s, a, rows, stream); break;
-        case 81: launch_split<G, 8, 1>(s, a, rows, stream); break;
-        case 161: launch_split<G, 16, 1>(s, a, rows, stream); break;
-        case 321: launch_split<G, 32, 1>(s, a, rows, stream); break;
-        case 641: launch_split<G, 64, 1>(s, a, rows, stream); break;
-        default: launch_split<G, 64, 2>(s, a, rows, stream); break;
+        case 41: launch_split<G, 4, 1, ROPE>(s, a, rows, stream); break;
+        case 81: launch_split<G, 8, 1, ROPE>(s, a, rows, stream); break;
+        case 161: launch_split<G, 16, 1, ROPE>(s, a, rows, stream); break;
+        case 321: launch_split<G, 32, 1, ROPE>(s, a, rows, stream); break;
+        case 641: launch_split<G, 64, 1, ROPE>(s, a, rows, stream); break;
+        default: launch_split<G, 64, 2, ROPE>(s, a, rows, stream); break;
     }
 }
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
 }  // namespace
 
@@ -669,9 +760,10 @@ bool attention_needs_scratch(const AttnShape& s, std::size_t rows, int kernel) {
     return resolve(kernel, rows, s) == kAttnSplit;
 }
 
-void run_attention(const AttnShape& s, int rows, const int* pos, const float* q, const float* kc,
-                   const float* vc, float* out, float* scratch, int kernel, hipStream_t stream) {
-    kernel = resolve(kernel, rows, s);
+namespace {
+
+AttnArgs base_args(const AttnShape& s, int rows, const int* pos, const float* q, const float* kc,
+                   const float* vc, float* out) {
     AttnArgs a{};
     a.n_heads = s.n_heads;
     a.head_size = s.head_size;
@@ -686,6 +778,23 @@ void run_attention(const AttnShape& s, int rows, const int* pos, const float* q,
     a.vc = vc;
     a.out = out;
     a.rows = rows;
+    return a;
+}
+
+void set_split(const AttnShape& s, int rows, float* scratch, AttnArgs& a) {
+    const SplitScratch l = split_scratch(s, rows);
+    a.splits = split_count(s.seq_len);
+    a.chunk_cap = split_chunk_cap(s);
+    a.part_o = scratch + l.o;
+    a.part_ml = reinterpret_cast<float2*>(scratch + l.ml);
+}
+
+}  // namespace
+
+void run_attention(const AttnShape& s, int rows, const int* pos, const float* q, const float* kc,
+                   const float* vc, float* out, float* scratch, int kernel, hipStream_t stream) {
+    kernel = resolve(kernel, rows, s);
+    AttnArgs a = base_args(s, rows, pos, q, kc, vc, out);
     if (kernel == kAttnTile) {
         launch_tile(s, a, rows, stream);
         return;
@@ -699,11 +808,7 @@ void run_attention(const AttnShape& s, int rows, const int* pos, const float* q,
         a.splits = 1;
         a.chunk_cap = s.seq_len;
     } else {
-        const SplitScratch l = split_scratch(s, rows);
-        a.splits = split_count(s.seq_len);
-        a.chunk_cap = split_chunk_cap(s);
-        a.part_o = scratch + l.o;
-        a.part_ml = reinterpret_cast<float2*>(scratch + l.ml);
+        set_split(s, rows, scratch, a);
     }
     switch (heads_per_block(s)) {
         case 8: launch_split_g<8>(s, a, rows, stream); break;
@@ -711,6 +816,31 @@ void run_attention(const AttnShape& s, int rows, const int* pos, const float* q,
         case 2: launch_split_g<2>(s, a, rows, stream); break;
         default: launch_split_g<1>(s, a, rows, stream); break;
     }
+}
+
+bool run_attention_rope(const AttnShape& s, const int* pos, const Summed& src, int dim,
+                        int kv_dim, const float* cos_t, const float* sin_t, float* kc, float* vc,
+                        float* out, float* scratch, hipStream_t stream) {
+    if (resolve(kAttnAutomatic, 1, s) != kAttnSplit || split_lds(s, true) > kMaxLds) return false;
+    if (src.n % 4 || src.mn % 4 || dim % 4 || kv_dim % 4) return false;
+    if (!aligned16(src.slices == 1 ? src.c : src.partial) || (src.scale && !aligned16(src.scale)))
+        return false;
+    AttnArgs a = base_args(s, 1, pos, nullptr, kc, vc, out);
+    set_split(s, 1, scratch, a);
+    a.src = src;
+    a.dim = dim;
+    a.kv_dim = kv_dim;
+    a.cos_t = cos_t;
+    a.sin_t = sin_t;
+    a.kc_w = kc;
+    a.vc_w = vc;
+    switch (heads_per_block(s)) {
+        case 8: launch_split_g<8, true>(s, a, 1, stream); break;
+        case 4: launch_split_g<4, true>(s, a, 1, stream); break;
+        case 2: launch_split_g<2, true>(s, a, 1, stream); break;
+        default: launch_split_g<1, true>(s, a, 1, stream); break;
+    }
+    return true;
 }
 
 }  // namespace em

@@ -138,6 +138,45 @@ __device__ __forceinline__ float summed(const Summed& s, int row, int col) {
     return t;
 }
 
+// One RoPE rotation of the pair (x0, x1) by the angle with cosine c and
+// sine s (model.cpp:93-103), with its two roundings spelled out, so that every
+// kernel that rotates a key (prefill, decode) caches the same bits.
+__device__ __forceinline__ float2 rope_pair(float x0, float x1, float c, float s) {
+    return make_float2(fmaf(x0, c, -(x1 * s)), fmaf(x0, s, x1 * c));
+}
+
+// summed() of four consecutive columns (col % 4 == 0, n % 4 == 0, 16-byte
+// aligned buffers): float4 loads, each component added in slice order as
+// ordered_sum adds it, then scaled: the same bits as four summed() calls.
+__device__ __forceinline__ floatx4 summed4(const Summed& s, int row, int col) {
+    const size_t idx = static_cast<size_t>(row) * s.n + col;
+    if (s.slices == 1) return *reinterpret_cast<const floatx4*>(s.c + idx);
+    const floatx4* p = reinterpret_cast<const floatx4*>(s.partial + idx);
+    const size_t stride4 = s.mn / 4;
+    floatx4 t{0.f, 0.f, 0.f, 0.f};
+    int sl = 0;
+    for (; sl + 16 <= s.slices; sl += 16) {
+        floatx4 v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = p[static_cast<size_t>(sl + i) * stride4];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) t += v[i];
+    }
+    if (sl < s.slices) {
+        const int left = s.slices - sl;
+        floatx4 v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (i < left) v[i] = p[static_cast<size_t>(sl + i) * stride4];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) t += v[i];
+    }
+    if (s.scale) t *= *reinterpret_cast<const floatx4*>(s.scale + col);
+    return t;
+}
+
 // SwiGLU of one (gate, up) pair, silu(g) * u (model.cpp:306-310): the one
 // expression every kernel that forms it uses, so they agree bit for bit.
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }

@@ -143,5 +143,15 @@ bool attention_needs_scratch(const AttnShape& s, std::size_t rows, int kernel);
 // Rows [0, rows) at positions *pos + i; the caller guarantees *pos + rows <= seq_len.
 void run_attention(const AttnShape& s, int rows, const int* pos, const float* q, const float* kc,
                    const float* vc, float* out, float* scratch, int kernel, hipStream_t stream);
+// One row at position *pos with the forward pass's RoPE and cache write
+// fused in: q, k, v are the columns [0, dim), [dim, dim + kv_dim) and
+// [dim + kv_dim, dim + 2 kv_dim) of the qkv product `src` (one row); q and k
+// are rotated with the tables' row *pos as rope_cache_kernel rotates them,
+// k and v are written to the caches at *pos, and out receives attention over
+// positions 0 .. *pos. Scratch as run_attention's for one row. False
+// (nothing launched) for a shape or alignment it does not take.
+bool run_attention_rope(const AttnShape& s, const int* pos, const Summed& src, int dim,
+                        int kv_dim, const float* cos_t, const float* sin_t, float* kc, float* vc,
+                        float* out, float* scratch, hipStream_t stream);
 
 }  // namespace em

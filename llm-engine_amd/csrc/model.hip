@@ -91,8 +91,8 @@ __global__ __launch_bounds__(kThreads) void rope_cache_kernel(Summed src, int qk
         const int a = pos * half + pair % half;
         const float c = cos_t[a], s = sin_t[a];
         const float x0 = summed(src, i, col), x1 = summed(src, i, col + 1);
-        const float y0 = x0 * c - x1 * s;
-        const float y1 = x0 * s + x1 * c;
+        const float2 y = rope_pair(x0, x1, c, s);
+        const float y0 = y.x, y1 = y.y;
         row[col] = y0;
         row[col + 1] = y1;
         if (is_k) {
@@ -439,11 +439,16 @@ void Model::enqueue(int n) {
     for (LayerDev& L : layers_) {
         const Summed qkv = project_summed(n, x_.p, L.wqkv, qkv_.p, L.rms_att.p,
                                           have_ssq ? ssq_.p : nullptr);
-        hipLaunchKernelGGL(rope_cache_kernel, dim3(ceil_div(rope_threads, kThreads), n),
-                           dim3(kThreads), 0, stream_, qkv, qkv_cols, D, KV, hs, feed_dev_.p,
-                           rope_cos_.p, rope_sin_.p, qkv_.p, L.kcache.p, L.vcache.p);
-        run_attention(shape_, n, feed_dev_.p, qkv_.p, L.kcache.p, L.vcache.p, att_.p,
-                      attn_scratch_.p, kAttnAutomatic, stream_);
+        // One row: RoPE and the cache write inside the attention launch.
+        if (!(n == 1 && run_attention_rope(shape_, feed_dev_.p, qkv, D, KV, rope_cos_.p,
+                                           rope_sin_.p, L.kcache.p, L.vcache.p, att_.p,
+                                           attn_scratch_.p, stream_))) {
+            hipLaunchKernelGGL(rope_cache_kernel, dim3(ceil_div(rope_threads, kThreads), n),
+                               dim3(kThreads), 0, stream_, qkv, qkv_cols, D, KV, hs, feed_dev_.p,
+                               rope_cos_.p, rope_sin_.p, qkv_.p, L.kcache.p, L.vcache.p);
+            run_attention(shape_, n, feed_dev_.p, qkv_.p, L.kcache.p, L.vcache.p, att_.p,
+                          attn_scratch_.p, kAttnAutomatic, stream_);
+        }
         have_ssq = residual(n, att_.p, L.wo);
         const Summed gu = project_summed(n, x_.p, L.w13, gu_.p, L.rms_ffn.p,
                                          have_ssq ? ssq_.p : nullptr);

@@ -71,6 +71,53 @@ def test_matches_cpu(tmp_path, heads, kv_heads, shared, wtype):
     gpu.close()
 
 
+@pytest.mark.parametrize("dim,hidden,heads,kv_heads,wtype",
+                         [(256, 688, 4, 2, "q8"), (256, 688, 4, 4, "f32"), (320, 864, 5, 5, "q8")],
+                         ids=["d256_gqa_q8", "d256_mha_f32", "d320_q8"])
+def test_norm_from_producer_sums_of_squares(tmp_path, dim, hidden, heads, kv_heads, wtype):
+    # A width that is a multiple of 64: one-token steps take each norm GEMV's
+    # scale from the sums of squares that embed and the residual reduces
+    # leave (the wo and w2 GEMVs split k here, so those reduces run), and
+    # rotate q and k inside the attention launch. Every decode over the
+    # context, then chunked and whole prefills (which take neither path),
+    # against the CPU Transformer.
+    #
+    # Tolerance: these logits reach ~20 (the reference fixture's, which its
+    # absolute 1e-4 is set for, are of order 1). fp32 results that differ
+    # only in summation order measured up to 1.0e-5 of the largest logit here
+    # on every GPU path, with or without the fused steps; the bound is 3e-5
+    # of it, and every decode's greedy token must equal the CPU's.
+    m = e2e_model.fixture_model(heads, kv_heads, False, seed=dim + heads, dim=dim,
+                                hidden=hidden, vocab=300, seq_len=24)
+    path = str(tmp_path / "model.bin")
+    e2e_model.write_raw(path, m)
+    ck = oracle.RefCheckpoint(lib, path)
+    q8 = wtype == "q8"
+    cpu = oracle.RefTransformer(lib, ck, q8)
+    gpu = em.Model(ck.config, ck.weights(), q8=q8)
+    T, V = ck.config["seq_len"], ck.config["vocab_size"]
+    tokens = [(p * 11 + 5) % V for p in range(T)]
+
+    def near(g, c, what):
+        tol = 3e-5 * float(np.abs(c).max())
+        d = float(np.abs(g - c).max())
+        assert d <= tol, f"{what}: max diff {d} > {tol}"
+        return d / tol
+
+    worst = 0.0
+    for pos in range(T):
+        print(f"dim {dim} {wtype} forward pos {pos}", flush=True)
+        g, c = gpu.forward(tokens[pos], pos), cpu.run([tokens[pos]], pos, True)
+        worst = max(worst, near(g, c, f"forward at {pos}"))
+        assert int(np.argmax(g)) == int(np.argmax(c)), f"greedy token at {pos}"
+    worst = max(worst, near(gpu.forward(tokens[:7], 0), cpu.run(tokens[:7], 0), "prefill 7"))
+    worst = max(worst, near(gpu.forward(tokens[7], 7), cpu.run([tokens[7]], 7, True),
+                            "forward after prefill"))
+    worst = max(worst, near(gpu.forward(tokens, 0), cpu.run(tokens, 0), "full prefill"))
+    print(f"dim {dim} {wtype}: worst logit diff {worst:.2f} of the bound")
+    gpu.close()
+
+
 def test_bad_inputs_then_cache_still_works(tmp_path):
     ck, w = load(tmp_path, 4, 2, True)
     gpu = em.Model(ck.config, w)
