@@ -348,9 +348,14 @@ def test_exact_split_tighter_than_fp32_tolerance(shape):
         assert ratio <= 1e-5, (kernel, ratio)
 
 
-@pytest.mark.parametrize("shape", [(40, 1000, 304), (256, 1000, 16384)], ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("shape", [(40, 1000, 304), (256, 1000, 16384), (300, 4096, 512),
+                                   (100, 6001, 272), (64, 8192, 256), (40, 12000, 64)],
+                         ids=lambda s: "x".join(map(str, s)))
 def test_exact_split_fused_norm_and_accumulate(shape):
-    # A narrow product split across k, and a wide one.
+    # A narrow product split across k, and a wide one; then rows the norm
+    # pre-pass holds in registers in one, two and four steps of 2048 values
+    # (6001: rows that are not 16-byte groups, loaded by scalars), and one
+    # past that (12000), which it reads twice.
     m, k, n = shape
     A = inputs.normal((m, k), 1.0, 511)
     w = inputs.uniform((k,), 0.5, 1.5, 512)
