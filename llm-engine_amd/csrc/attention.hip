@@ -549,10 +549,17 @@ __global__ __launch_bounds__(kThreads) void attn_single_kernel(AttnArgs a) {
 //  * Every accumulator of a lane belongs to query j: the online softmax
 //    rescale is one factor per lane. The block max takes two xor shuffles
 //    (the four lane groups of a query); the sum is combined once, at the end.
-// Positions past a query's own are masked, and blocks past the wave's last
+// Positions past a query's own are masked, and blocks past the tile's last
 // row are never read; the next block's keys and values are loaded while
 // this one is used (two register sets, alternating; a 32-position block
 // measured no faster and needs twice the registers).
+//
+// A workgroup is four such waves on one (head, 16-row tile): wave w takes
+// the w-th quarter of the tile's blocks, keeping its own online softmax, and
+// the four are merged in LDS in wave order at the end. Causal tiles differ
+// in length up to 32-fold at 512 rows, and with one wave per tile the
+// longest set the kernel's time. A query with no position in a wave's
+// quarter leaves that wave's m = -inf, l = 0, O = 0.
 template <int E>
 struct TileBlock {
     floatx4 k[E];   // K[t0 + j][4E g .. 4E g + 4E)
@@ -583,12 +590,19 @@ __device__ __forceinline__ void load_run(const float* src, float* dst) {
     }
 }
 
+constexpr int kTileWaves = 4;
+
 template <int E>
-__global__ __launch_bounds__(kWave) void attn_tile_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kTileWaves * kWave) void attn_tile_kernel(AttnArgs a) {
     constexpr int HS = 16 * E, Q4 = 4 * E;
     constexpr int KB = 16;  // positions per block
-    const int lane = threadIdx.x, g = lane >> 4, j = lane & 15;
-    const int h = blockIdx.x, r0 = blockIdx.y * kTileRows;
+    __shared__ float ms[kTileWaves][kWave], ls[kTileWaves][kWave];
+    __shared__ floatx4 os[kTileWaves][E][kWave];
+    const int lane = threadIdx.x % kWave, g = lane >> 4, j = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    // Row tiles in reverse: the longest (causal) start first and the short
+    // ones fill in behind them.
+    const int h = blockIdx.x, r0 = (gridDim.y - 1 - blockIdx.y) * kTileRows;
     const int pos0 = *a.pos;
     const int row = min(r0 + j, a.rows - 1);  // rows past the call: computed, not stored
     const int pq = pos0 + row;                // this lane's query position
@@ -639,16 +653,17 @@ __global__ __launch_bounds__(kWave) void attn_tile_kernel(AttnArgs a) {
         }
         mb = fmaxf(mb, __shfl_xor(mb, 16, kWave));
         mb = fmaxf(mb, __shfl_xor(mb, 32, kWave));
-        // Position 0 is in every query's context, so mn is finite from the
-        // first block on; before it, m = -inf gives alpha = 0.
+        // mn = -inf: no position of this query yet (its position precedes
+        // the wave's blocks so far); everything stays as it is.
         const float mn = fmaxf(m, mb);
-        const float alpha = expf(m - mn);
+        const bool none = mn == -INFINITY;
+        const float alpha = none ? 1.0f : expf(m - mn);
         l *= alpha;
 #pragma unroll
         for (int c = 0; c < E; ++c) o[c] *= alpha;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float p = expf(sv[r] - mn);
+            const float p = none ? 0.0f : expf(sv[r] - mn);
             l += p;
 #pragma unroll
             for (int c = 0; c < E; ++c) o[c] = mfma16x16x4(b.v[r][c], p, o[c]);
@@ -656,14 +671,42 @@ __global__ __launch_bounds__(kWave) void attn_tile_kernel(AttnArgs a) {
         m = mn;
     };
 
-    TileBlock<E> b0, b1;
-    load(b0, 0);
-    for (int t0 = 0; t0 <= last; t0 += 2 * KB) {
-        if (t0 + KB <= last) load(b1, t0 + KB);
-        use(b0, t0);
-        if (t0 + KB > last) break;
-        if (t0 + 2 * KB <= last) load(b0, t0 + 2 * KB);
-        use(b1, t0 + KB);
+    // This wave's blocks: [nb * w / 4, nb * (w + 1) / 4) of the tile's nb.
+    const int nb = last / KB + 1;
+    const int first = KB * (nb * wave / kTileWaves);
+    const int wlast = KB * (nb * (wave + 1) / kTileWaves) - 1;  // < first: no blocks
+    if (first <= wlast) {
+        TileBlock<E> b0, b1;
+        load(b0, first);
+        for (int t0 = first; t0 <= wlast; t0 += 2 * KB) {
+            if (t0 + KB <= wlast) load(b1, t0 + KB);
+            use(b0, t0);
+            if (t0 + KB > wlast) break;
+            if (t0 + 2 * KB <= wlast) load(b0, t0 + 2 * KB);
+            use(b1, t0 + KB);
+        }
+    }
+
+    // Merge the waves in order: lane l of every wave holds query j's state.
+    ms[wave][lane] = m;
+    ls[wave][lane] = l;
+#pragma unroll
+    for (int c = 0; c < E; ++c) os[wave][c][lane] = o[c];
+    __syncthreads();
+    if (wave != 0) return;
+    float M = ms[0][lane];
+#pragma unroll
+    for (int w = 1; w < kTileWaves; ++w) M = fmaxf(M, ms[w][lane]);  // finite: wave 0 has position 0
+    l = 0.0f;
+#pragma unroll
+    for (int c = 0; c < E; ++c) o[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kTileWaves; ++w) {
+        const float mw = ms[w][lane];
+        const float f = mw == -INFINITY ? 0.0f : expf(mw - M);
+        l += f * ls[w][lane];
+#pragma unroll
+        for (int c = 0; c < E; ++c) o[c] += f * os[w][c][lane];
     }
 
     // The four lane groups of query j hold partial sums of its denominator;
@@ -687,15 +730,16 @@ __global__ __launch_bounds__(kWave) void attn_tile_kernel(AttnArgs a) {
 
 void launch_tile(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t stream) {
     const dim3 grid(s.n_heads, (rows + kTileRows - 1) / kTileRows);
+    const dim3 block(kTileWaves * kWave);
     switch (s.head_size / 16) {
-        case 1: hipLaunchKernelGGL(attn_tile_kernel<1>, grid, dim3(kWave), 0, stream, a); break;
-        case 2: hipLaunchKernelGGL(attn_tile_kernel<2>, grid, dim3(kWave), 0, stream, a); break;
-        case 3: hipLaunchKernelGGL(attn_tile_kernel<3>, grid, dim3(kWave), 0, stream, a); break;
-        case 4: hipLaunchKernelGGL(attn_tile_kernel<4>, grid, dim3(kWave), 0, stream, a); break;
-        case 5: hipLaunchKernelGGL(attn_tile_kernel<5>, grid, dim3(kWave), 0, stream, a); break;
-        case 6: hipLaunchKernelGGL(attn_tile_kernel<6>, grid, dim3(kWave), 0, stream, a); break;
-        case 7: hipLaunchKernelGGL(attn_tile_kernel<7>, grid, dim3(kWave), 0, stream, a); break;
-        default: hipLaunchKernelGGL(attn_tile_kernel<8>, grid, dim3(kWave), 0, stream, a); break;
+        case 1: hipLaunchKernelGGL(attn_tile_kernel<1>, grid, block, 0, stream, a); break;
+        case 2: hipLaunchKernelGGL(attn_tile_kernel<2>, grid, block, 0, stream, a); break;
+        case 3: hipLaunchKernelGGL(attn_tile_kernel<3>, grid, block, 0, stream, a); break;
+        case 4: hipLaunchKernelGGL(attn_tile_kernel<4>, grid, block, 0, stream, a); break;
+        case 5: hipLaunchKernelGGL(attn_tile_kernel<5>, grid, block, 0, stream, a); break;
+        case 6: hipLaunchKernelGGL(attn_tile_kernel<6>, grid, block, 0, stream, a); break;
+        case 7: hipLaunchKernelGGL(attn_tile_kernel<7>, grid, block, 0, stream, a); break;
+        default: hipLaunchKernelGGL(attn_tile_kernel<8>, grid, block, 0, stream, a); break;
     }
 }
 
