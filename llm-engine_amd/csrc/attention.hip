@@ -383,12 +383,14 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
 
 // Merges the chunks of one (head, row): m = max m_c,
 // l = sum e^(m_c - m) l_c, out = sum e^(m_c - m) o_c / l. The hs4 threads
-// of a slot take chunks r, r + slots, ... (eight loads in flight), and the
-// slots are added in LDS in slot order, so the result is the same on every
+// of a slot take chunks r, r + slots, ... (eight loads in flight) and keep
+// their own running max, sum and output over them (rescaled between
+// batches of eight); the slots are then combined in slot order, each scaled
+// by e^(its max - m). One barrier: a block-wide max first would cost two
+// more, and the loads do not depend on it. The result is the same on every
 // call.
 __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
-    __shared__ float part[4];
-    extern __shared__ floatx4 red4[];  // slots x hs4 values, then slots sums
+    extern __shared__ floatx4 red4[];  // slots x hs4 outputs, then slots x (max, sum)
     const int h = blockIdx.x, i = blockIdx.y;
     const int n_ctx = *a.pos + i + 1;
     const int chunk = chunk_size(n_ctx, a.splits);
@@ -399,57 +401,53 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
     const int hs4 = a.head_size / 4;
     const int slots = kThreads / hs4, r = tid / hs4, d = tid % hs4;
     const floatx4* po = reinterpret_cast<const floatx4*>(a.part_o);
-    float* red_l = reinterpret_cast<float*>(red4 + slots * hs4);
-    const bool worker = r < slots;
+    float2* red_ml = reinterpret_cast<float2*>(red4 + slots * hs4);
 
-    // The first eight splits' (max, sum) and outputs are loaded before the
-    // block max is formed: they do not depend on it, so the merge waits on
-    // one memory latency instead of two.
-    float2 ml[8];
-    floatx4 o[8];
-    if (worker) {
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int c = min(r + u * slots, n - 1);
-            ml[u] = a.part_ml[b + c];
-            o[u] = po[(b + c) * hs4 + d];
-        }
-    }
-    float mloc = -INFINITY;
-    for (int c = tid; c < n; c += kThreads) mloc = fmaxf(mloc, a.part_ml[b + c].x);
-    const float M = block_max(mloc, part);
-
-    if (worker) {
+    if (r < slots) {
+        float m = -INFINITY, l = 0.0f;
         floatx4 acc{0.f, 0.f, 0.f, 0.f};
-        float l = 0.0f;
         for (int c0 = r; c0 < n; c0 += 8 * slots) {
-            if (c0 != r) {
+            float2 ml[8];
+            floatx4 o[8];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int c = min(c0 + u * slots, n - 1);
-                    ml[u] = a.part_ml[b + c];
-                    o[u] = po[(b + c) * hs4 + d];
-                }
+            for (int u = 0; u < 8; ++u) {
+                const int c = min(c0 + u * slots, n - 1);
+                ml[u] = a.part_ml[b + c];
+                o[u] = po[(b + c) * hs4 + d];
             }
+            float mb = m;
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (c0 + u * slots < n) mb = fmaxf(mb, ml[u].x);
+            // mb is finite: chunk c0 < n holds at least one position.
+            const float alpha = expf(m - mb);  // 0 while m = -inf
+            l *= alpha;
+            acc *= alpha;
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 if (c0 + u * slots < n) {
-                    const float w = expf(ml[u].x - M);
+                    const float w = expf(ml[u].x - mb);
                     l += w * ml[u].y;
                     acc += w * o[u];
                 }
             }
+            m = mb;
         }
         red4[r * hs4 + d] = acc;
-        if (d == 0) red_l[r] = l;
+        if (d == 0) red_ml[r] = make_float2(m, l);
     }
     __syncthreads();
     if (tid < hs4) {
-        floatx4 total = red4[tid];
-        float l = red_l[0];
-        for (int rr = 1; rr < slots; ++rr) {
-            total += red4[rr * hs4 + tid];
-            l += red_l[rr];
+        const int used = min(slots, n);  // slots past n saw no chunk
+        float M = red_ml[0].x;
+        for (int rr = 1; rr < used; ++rr) M = fmaxf(M, red_ml[rr].x);
+        floatx4 total{0.f, 0.f, 0.f, 0.f};
+        float l = 0.0f;
+        for (int rr = 0; rr < used; ++rr) {
+            const float2 ml = red_ml[rr];
+            const float f = expf(ml.x - M);
+            total += f * red4[rr * hs4 + tid];
+            l += f * ml.y;
         }
         reinterpret_cast<floatx4*>(a.out + static_cast<std::size_t>(i) * a.out_stride +
                                    static_cast<std::size_t>(h) * a.head_size)[tid] =
@@ -751,7 +749,7 @@ void launch_split(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t s
     if (a.splits == 1) return;  // one chunk per row: written directly
     const std::size_t hs4 = s.head_size / 4, slots = kThreads / hs4;
     hipLaunchKernelGGL(attn_merge_kernel, dim3(s.n_heads, rows), dim3(kThreads),
-                       (slots * hs4 * 4 + slots) * sizeof(float), stream, a);
+                       (slots * hs4 * 4 + 2 * slots) * sizeof(float), stream, a);
 }
 
 template <int G, bool ROPE = false>
