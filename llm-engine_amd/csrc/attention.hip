@@ -189,6 +189,38 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
     const bool own_pos = ROPE && s == nchunks - 1;
     const int loop_len = own_pos ? len - 1 : len;
     float* rq = lds + G * NS * hs + 2 * G * NS;  // ROPE: G rotated queries, key, value
+
+    // This lane's columns; lanes past hs4 read the last column with a zero
+    // query and store nothing.
+    int dcol[F];
+    bool dok[F];
+#pragma unroll
+    for (int f = 0; f < F; ++f) {
+        const int d = sub + f * LPP;
+        dok[f] = d < hs4;
+        dcol[f] = dok[f] ? d : hs4 - 1;
+    }
+    const float* kbase = a.kc + static_cast<std::size_t>(t0) * a.kv_stride + kv_off;
+    const float* vbase = a.vc + static_cast<std::size_t>(t0) * a.kv_stride + kv_off;
+    // Every key and value of a round in flight; positions past the chunk
+    // re-read its last position and are masked. (Issuing the first round
+    // before the ROPE query is formed measured 1 us slower at ctx 512: the
+    // query's loads then wait behind the whole chunk's.)
+    floatx4 kv[PP][F], vv[PP][F];
+    auto load_round = [&](int b0) {
+#pragma unroll
+        for (int pp = 0; pp < PP; ++pp) {
+            const int t = min(b0 + slot + pp * NS, loop_len - 1);
+            const floatx4* kr = reinterpret_cast<const floatx4*>(kbase + static_cast<std::size_t>(t) * a.kv_stride);
+            const floatx4* vr = reinterpret_cast<const floatx4*>(vbase + static_cast<std::size_t>(t) * a.kv_stride);
+#pragma unroll
+            for (int f = 0; f < F; ++f) {
+                kv[pp][f] = kr[dcol[f]];
+                vv[pp][f] = vr[dcol[f]];
+            }
+        }
+    };
+
     if constexpr (ROPE) {
         const int pos = n_ctx - 1, half = hs / 2;
         const float* cs = a.cos_t + static_cast<std::size_t>(pos) * half;
@@ -209,11 +241,15 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
                 col = a.dim + a.kv_dim + kv_off + 4 * d;
                 rot = false;
             }
+            // The angles are loaded for values too (d < hs4, so in range) and
+            // before the product's slices: one wait covers every load here
+            // and the first round of keys and values.
+            const float c0 = cs[2 * d], s0 = sn[2 * d], c1 = cs[2 * d + 1], s1 = sn[2 * d + 1];
             const floatx4 x = summed4(a.src, 0, col);
             floatx4 y = x;
             if (rot) {
-                const float2 r0 = rope_pair(x.x, x.y, cs[2 * d], sn[2 * d]);
-                const float2 r1 = rope_pair(x.z, x.w, cs[2 * d + 1], sn[2 * d + 1]);
+                const float2 r0 = rope_pair(x.x, x.y, c0, s0);
+                const float2 r1 = rope_pair(x.z, x.w, c1, s1);
                 y = floatx4{r0.x, r0.y, r1.x, r1.y};
             }
             reinterpret_cast<floatx4*>(rq)[j] = y;
@@ -226,16 +262,6 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
         __syncthreads();
     }
 
-    // This lane's columns; lanes past hs4 read the last column with a zero
-    // query and store nothing.
-    int dcol[F];
-    bool dok[F];
-#pragma unroll
-    for (int f = 0; f < F; ++f) {
-        const int d = sub + f * LPP;
-        dok[f] = d < hs4;
-        dcol[f] = dok[f] ? d : hs4 - 1;
-    }
     floatx4 q[G][F];
     const float* qrow = ROPE ? rq : a.q + static_cast<std::size_t>(i) * a.q_stride +
                                         static_cast<std::size_t>(h0) * hs;
@@ -257,23 +283,8 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
         for (int f = 0; f < F; ++f) o[g][f] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
 
-    const float* kbase = a.kc + static_cast<std::size_t>(t0) * a.kv_stride + kv_off;
-    const float* vbase = a.vc + static_cast<std::size_t>(t0) * a.kv_stride + kv_off;
     for (int b0 = 0; b0 < loop_len; b0 += ROUND) {
-        // Every key and value of the round in flight; positions past the
-        // chunk re-read its last position and are masked below.
-        floatx4 kv[PP][F], vv[PP][F];
-#pragma unroll
-        for (int pp = 0; pp < PP; ++pp) {
-            const int t = min(b0 + slot + pp * NS, loop_len - 1);
-            const floatx4* kr = reinterpret_cast<const floatx4*>(kbase + static_cast<std::size_t>(t) * a.kv_stride);
-            const floatx4* vr = reinterpret_cast<const floatx4*>(vbase + static_cast<std::size_t>(t) * a.kv_stride);
-#pragma unroll
-            for (int f = 0; f < F; ++f) {
-                kv[pp][f] = kr[dcol[f]];
-                vv[pp][f] = vr[dcol[f]];
-            }
-        }
+        load_round(b0);
         float sc[G][PP];
 #pragma unroll
         for (int pp = 0; pp < PP; ++pp) {
