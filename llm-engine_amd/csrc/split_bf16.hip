@@ -430,13 +430,21 @@ void run_split_bf16(const MatmulArgs& a) {
         const int x = v ? std::atoi(v) : 0;
         return x == 1 || x == 2 || x == 4 ? x : 0;
     }();
-    // One 16-row block per workgroup keeps the most workgroups in flight and
-    // measured fastest up to m = 256; past that, more blocks per workgroup
-    // cut how often each weight is widened (4096^2: two blocks at m = 512,
-    // 49 vs 61 us for one; four from m = 1024, 90 vs 95 us for two).
-    const int RB = forced_rb ? forced_rb : a.m <= 256 ? 1 : a.m < 1024 ? 2 : 4;
-    const int row_tiles = ceil_div(a.m, 16 * RB);
+    // More 16-row blocks per workgroup cut how often each weight is widened
+    // (the VALU work that paces this kernel); fewer keep more workgroups in
+    // flight without a k split and its reduce. The largest of 4 / 2 / 1
+    // whose tile grid, weighted by k / 4096 (deeper k holds more work per
+    // workgroup), reaches 160 was within 5 % of the best of the three in a
+    // sweep of m = 128..1024 over the Llama-7B shapes. At m = 512: 4096^2
+    // takes 2 (55 vs 64 us for 4), 4096 x 22016 with the norm 4 (296 vs 342
+    // us for 2), 4096 x 32000 4 (375 vs 441).
     const int col_tiles = ceil_div(a.n, kTile);
+    const double kf = std::max(1.0, a.k / 4096.0);
+    auto fits = [&](int rb) {
+        return 16 * rb <= a.m + 15 && ceil_div(a.m, 16 * rb) * static_cast<double>(col_tiles) * kf >= 160.0;
+    };
+    const int RB = forced_rb ? forced_rb : fits(4) ? 4 : fits(2) ? 2 : 1;
+    const int row_tiles = ceil_div(a.m, 16 * RB);
     const int m_pad = row_tiles * 16 * RB;
     const int k_pad = ceil_div(a.k, kChunk) * kChunk;
 
