@@ -34,6 +34,7 @@
 //    sets per wave; the epilogue stages the four waves' sums in LDS and
 //    writes coalesced float4 runs; k slices go through reduce_slices.
 #include <algorithm>
+#include <cmath>
 #include <cstdlib>
 
 #include "common.hpp"
@@ -430,28 +431,38 @@ void run_split_bf16(const MatmulArgs& a) {
         const int x = v ? std::atoi(v) : 0;
         return x == 1 || x == 2 || x == 4 ? x : 0;
     }();
+    // Without a norm, the kernel splits A itself, chunk by chunk (needs whole
+    // 8-value groups and 16-byte rows); otherwise a pre-pass writes the three
+    // planes with the norm fused.
+    const bool raw = !a.rms_weight && a.k % 8 == 0 && reinterpret_cast<uintptr_t>(a.A) % 16 == 0;
+
     // More 16-row blocks per workgroup cut how often each weight is widened
     // (the VALU work that paces this kernel); fewer keep more workgroups in
-    // flight without a k split and its reduce. The largest of 4 / 2 / 1
-    // whose tile grid, weighted by k / 4096 (deeper k holds more work per
-    // workgroup), reaches 160 was within 5 % of the best of the three in a
-    // sweep of m = 128..1024 over the Llama-7B shapes. At m = 512: 4096^2
-    // takes 2 (55 vs 64 us for 4), 4096 x 22016 with the norm 4 (296 vs 342
-    // us for 2), 4096 x 32000 4 (375 vs 441).
+    // flight without a k split and its reduce, and round the grid better
+    // (one workgroup per CU at a time). The largest of 4 / 2 / 1 whose tile
+    // grid, weighted by k / 4096 (deeper k holds more work per workgroup),
+    // reaches 160 workgroups and, past one per CU, leaves its last round at
+    // least 80 % full (70 % with A pre-split into planes, where a workgroup
+    // splits nothing itself and widening weighs more). Over sweeps of
+    // m = 128..1024 and 15 shapes (widths 4096..32000, k 4096 and 11008,
+    // with and without the norm) it averaged 0.6 % above the best of the
+    // three, at most 8 %. At m = 512: 4096^2 takes 2 (55 vs 64 us for 4),
+    // 4096 x 11008 2 (162 vs 177), 4096 x 22016 4 (266 vs 294), 4096 x 32000
+    // 4 (362 vs 408).
     const int col_tiles = ceil_div(a.n, kTile);
     const double kf = std::max(1.0, a.k / 4096.0);
     auto fits = [&](int rb) {
-        return 16 * rb <= a.m + 15 && ceil_div(a.m, 16 * rb) * static_cast<double>(col_tiles) * kf >= 160.0;
+        if (16 * rb > a.m + 15) return false;
+        const double grid = static_cast<double>(ceil_div(a.m, 16 * rb)) * col_tiles;
+        if (grid * kf < 160.0) return false;
+        const double rounds = grid / cu_count();
+        return rounds <= 1.0 || rounds / std::ceil(rounds) >= (raw ? 0.8 : 0.7);
     };
     const int RB = forced_rb ? forced_rb : fits(4) ? 4 : fits(2) ? 2 : 1;
     const int row_tiles = ceil_div(a.m, 16 * RB);
     const int m_pad = row_tiles * 16 * RB;
     const int k_pad = ceil_div(a.k, kChunk) * kChunk;
 
-    // Without a norm, the kernel splits A itself, chunk by chunk (needs whole
-    // 8-value groups and 16-byte rows); otherwise a pre-pass writes the three
-    // planes with the norm fused.
-    const bool raw = !a.rms_weight && a.k % 8 == 0 && reinterpret_cast<uintptr_t>(a.A) % 16 == 0;
     uint16_t* A3 = nullptr;
     if (!raw) {
         A3 = reinterpret_cast<uint16_t*>(
