@@ -73,7 +73,8 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(int dim, const int* __r
 // pair of q and k by the position's angles, as rope() does (model.cpp:93-103),
 // then writes the rotated k and the v slice into the caches (model.cpp:297-
 // 299). A thread takes one q pair, one k pair or one v element; src yields
-// the qkv product (qkv_cols wide), which is stored back to qkv rotated.
+// the qkv product (qkv_cols wide). Only the rotated q goes back into the qkv
+// row: attention reads keys and values from the caches.
 __global__ __launch_bounds__(kThreads) void rope_cache_kernel(Summed src, int qkv_cols, int dim,
                                                               int kv_dim, int head_size,
                                                               const int* feed, const float* cos_t,
@@ -92,19 +93,14 @@ __global__ __launch_bounds__(kThreads) void rope_cache_kernel(Summed src, int qk
         const float c = cos_t[a], s = sin_t[a];
         const float x0 = summed(src, i, col), x1 = summed(src, i, col + 1);
         const float2 y = rope_pair(x0, x1, c, s);
-        const float y0 = y.x, y1 = y.y;
-        row[col] = y0;
-        row[col + 1] = y1;
-        if (is_k) {
-            float* dst = key_cache + static_cast<std::size_t>(pos) * kv_dim + 2 * pair;
-            dst[0] = y0;
-            dst[1] = y1;
-        }
+        float* dst = is_k ? key_cache + static_cast<std::size_t>(pos) * kv_dim + 2 * pair
+                          : row + col;
+        dst[0] = y.x;
+        dst[1] = y.y;
     } else if (j < nq + nk + kv_dim) {
         const int t = j - nq - nk;
-        const float val = summed(src, i, dim + kv_dim + t);
-        row[dim + kv_dim + t] = val;
-        value_cache[static_cast<std::size_t>(pos) * kv_dim + t] = val;
+        value_cache[static_cast<std::size_t>(pos) * kv_dim + t] =
+            summed(src, i, dim + kv_dim + t);
     }
 }
 
