@@ -72,8 +72,9 @@ def test_matches_cpu(tmp_path, heads, kv_heads, shared, wtype):
 
 
 @pytest.mark.parametrize("dim,hidden,heads,kv_heads,wtype",
-                         [(256, 688, 4, 2, "q8"), (256, 688, 4, 4, "f32"), (320, 864, 5, 5, "q8")],
-                         ids=["d256_gqa_q8", "d256_mha_f32", "d320_q8"])
+                         [(256, 688, 4, 2, "q8"), (256, 688, 4, 4, "f32"), (320, 864, 5, 5, "q8"),
+                          (192, 512, 6, 2, "q8")],
+                         ids=["d256_gqa_q8", "d256_mha_f32", "d320_q8", "d192_group3_q8"])
 def test_norm_from_producer_sums_of_squares(tmp_path, dim, hidden, heads, kv_heads, wtype):
     # A width that is a multiple of 64: one-token steps take each norm GEMV's
     # scale from the sums of squares that embed and the residual reduces
@@ -81,6 +82,9 @@ def test_norm_from_producer_sums_of_squares(tmp_path, dim, hidden, heads, kv_hea
     # rotate q and k inside the attention launch. Every decode over the
     # context, then chunked and whole prefills (which take neither path),
     # against the CPU Transformer.
+    #
+    # d192_group3: three query heads per kv head, one per split workgroup,
+    # so only the first of them writes the current key and value.
     #
     # Tolerance: these logits reach ~20 (the reference fixture's, which its
     # absolute 1e-4 is set for, are of order 1). fp32 results that differ
