@@ -442,7 +442,10 @@ int rows_per_lane(int E, int m, int n, int k) {
     if (E == 1) return 16;
     const int mm = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
     const int cap = max_depth(E, mm);
-    int L = 4;
+    // Too few columns and rows for half a workgroup per CU: fp32 lanes still
+    // take 8 rows (4 would make 16-row slices, 18 of them at k = 288: the
+    // stories15M fp32 decode ran 0.217 ms/token against 0.198 at 8).
+    int L = E == 4 ? 8 : 4;
     if (forced == 4 || forced == 8 || forced == 16 || forced == 32) {
         L = forced;
     } else if (k <= E * cap && ceil_div(n, kThreads) >= cu_count() / 4) {
