@@ -393,50 +393,60 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
 }
 
 // Merges the chunks of one (head, row): m = max m_c,
-// l = sum e^(m_c - m) l_c, out = sum e^(m_c - m) o_c / l. The hs4 threads
-// of a slot take chunks r, r + slots, ... (eight loads in flight) and keep
-// their own running max, sum and output over them (rescaled between
-// batches of eight); the slots are then combined in slot order, each scaled
-// by e^(its max - m). One barrier: a block-wide max first would cost two
-// more, and the loads do not depend on it. The result is the same on every
-// call.
+// l = sum e^(m_c - m) l_c, out = sum e^(m_c - m) o_c / l. A workgroup takes
+// kMergeDims float4s of the head's columns (blockIdx.x = head * groups +
+// group), so a long context's chunks spread over more workgroups. As many
+// slots work as eight chunks each need (up to 256 / dpw): the dpw threads of
+// slot r take chunks r, r + used, ..., loaded in one batch, and keep their
+// own max, sum and output over them; the slots are then combined in slot
+// order, each scaled by e^(its max - m), after one barrier. The result is
+// the same on every call. (One workgroup per head took 8.7 us for 32 heads
+// x 256 chunks: four dependent batches in each of 32 workgroups; always
+// using every slot made 64 chunks slower, a 32-step combine.)
+constexpr int kMergeDims = 8;
+
 __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
-    extern __shared__ floatx4 red4[];  // slots x hs4 outputs, then slots x (max, sum)
-    const int h = blockIdx.x, i = blockIdx.y;
+    extern __shared__ floatx4 red4[];  // slots x dpw outputs, then slots x (max, sum)
+    const int hs4 = a.head_size / 4;
+    const int dpw = hs4 < kMergeDims ? hs4 : kMergeDims, groups = (hs4 + dpw - 1) / dpw;
+    const int h = blockIdx.x / groups, d0 = (blockIdx.x % groups) * dpw;
+    const int i = blockIdx.y;
     const int n_ctx = *a.pos + i + 1;
     const int chunk = chunk_size(n_ctx, a.splits);
     const int n = (n_ctx + chunk - 1) / chunk;
     if (n == 1) return;  // written by the split kernel
     const std::size_t b = (static_cast<std::size_t>(i) * a.n_heads + h) * a.splits;
     const int tid = threadIdx.x;
-    const int hs4 = a.head_size / 4;
-    const int slots = kThreads / hs4, r = tid / hs4, d = tid % hs4;
+    const int slots = kThreads / dpw, r = tid / dpw, dd = tid % dpw, d = d0 + dd;
+    const bool dok = d < hs4;
+    const int dl = dok ? d : hs4 - 1;  // past the head: computed, not stored
     const floatx4* po = reinterpret_cast<const floatx4*>(a.part_o);
-    float2* red_ml = reinterpret_cast<float2*>(red4 + slots * hs4);
+    float2* red_ml = reinterpret_cast<float2*>(red4 + slots * dpw);
+    const int used = min(slots, (n + 7) / 8);  // slots that take chunks
 
-    if (r < slots) {
+    if (r < used) {
         float m = -INFINITY, l = 0.0f;
         floatx4 acc{0.f, 0.f, 0.f, 0.f};
-        for (int c0 = r; c0 < n; c0 += 8 * slots) {
+        for (int c0 = r; c0 < n; c0 += 8 * used) {
             float2 ml[8];
             floatx4 o[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                const int c = min(c0 + u * slots, n - 1);
+                const int c = min(c0 + u * used, n - 1);
                 ml[u] = a.part_ml[b + c];
-                o[u] = po[(b + c) * hs4 + d];
+                o[u] = po[(b + c) * hs4 + dl];
             }
             float mb = m;
 #pragma unroll
             for (int u = 0; u < 8; ++u)
-                if (c0 + u * slots < n) mb = fmaxf(mb, ml[u].x);
+                if (c0 + u * used < n) mb = fmaxf(mb, ml[u].x);
             // mb is finite: chunk c0 < n holds at least one position.
             const float alpha = expf(m - mb);  // 0 while m = -inf
             l *= alpha;
             acc *= alpha;
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                if (c0 + u * slots < n) {
+                if (c0 + u * used < n) {
                     const float w = expf(ml[u].x - mb);
                     l += w * ml[u].y;
                     acc += w * o[u];
@@ -444,12 +454,11 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
             }
             m = mb;
         }
-        red4[r * hs4 + d] = acc;
-        if (d == 0) red_ml[r] = make_float2(m, l);
+        red4[r * dpw + dd] = acc;
+        if (dd == 0) red_ml[r] = make_float2(m, l);
     }
     __syncthreads();
-    if (tid < hs4) {
-        const int used = min(slots, n);  // slots past n saw no chunk
+    if (tid < dpw && dok) {
         float M = red_ml[0].x;
         for (int rr = 1; rr < used; ++rr) M = fmaxf(M, red_ml[rr].x);
         floatx4 total{0.f, 0.f, 0.f, 0.f};
@@ -457,11 +466,11 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
         for (int rr = 0; rr < used; ++rr) {
             const float2 ml = red_ml[rr];
             const float f = expf(ml.x - M);
-            total += f * red4[rr * hs4 + tid];
+            total += f * red4[rr * dpw + tid];
             l += f * ml.y;
         }
         reinterpret_cast<floatx4*>(a.out + static_cast<std::size_t>(i) * a.out_stride +
-                                   static_cast<std::size_t>(h) * a.head_size)[tid] =
+                                   static_cast<std::size_t>(h) * a.head_size)[d] =
             total * (1.0f / l);
     }
 }
@@ -758,9 +767,11 @@ void launch_split(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t s
     hipLaunchKernelGGL((attn_split_kernel<G, LPP, F, ROPE>), grid, dim3(kThreads),
                        split_lds(s, ROPE), stream, a);
     if (a.splits == 1) return;  // one chunk per row: written directly
-    const std::size_t hs4 = s.head_size / 4, slots = kThreads / hs4;
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(s.n_heads, rows), dim3(kThreads),
-                       (slots * hs4 * 4 + 2 * slots) * sizeof(float), stream, a);
+    const int hs4 = s.head_size / 4;
+    const int dpw = hs4 < kMergeDims ? hs4 : kMergeDims, groups = (hs4 + dpw - 1) / dpw;
+    const std::size_t slots = kThreads / dpw;
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(s.n_heads * groups, rows), dim3(kThreads),
+                       (slots * dpw * 4 + 2 * slots) * sizeof(float), stream, a);
 }
 
 template <int G, bool ROPE = false>
