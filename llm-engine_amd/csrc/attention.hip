@@ -40,7 +40,7 @@
 namespace em {
 namespace {
 
-constexpr int kMinChunk = 64;           // positions per split workgroup, at least
+constexpr int kMinChunk = kSplitMinChunk;  // positions per split workgroup, at least
 constexpr int kMaxSplits = 256;         // chunks per (row, head group), at most
 constexpr std::size_t kSplitMaxRows = 8;   // automatic: split up to this many rows
 constexpr std::size_t kMaxLds = 64 * 1024;  // dynamic LDS per workgroup
@@ -51,8 +51,7 @@ int split_count(int seq_len) {
 }
 
 __host__ __device__ __forceinline__ int chunk_size(int n_ctx, int splits) {
-    const int c = (n_ctx + splits - 1) / splits;
-    return c > kMinChunk ? c : kMinChunk;
+    return split_chunk(n_ctx, splits);
 }
 
 int split_chunk_cap(const AttnShape& s) { return chunk_size(s.seq_len, split_count(s.seq_len)); }
@@ -436,42 +435,18 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
                 ml[u] = a.part_ml[b + c];
                 o[u] = po[(b + c) * hs4 + dl];
             }
-            float mb = m;
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                if (c0 + u * used < n) mb = fmaxf(mb, ml[u].x);
-            // mb is finite: chunk c0 < n holds at least one position.
-            const float alpha = expf(m - mb);  // 0 while m = -inf
-            l *= alpha;
-            acc *= alpha;
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                if (c0 + u * used < n) {
-                    const float w = expf(ml[u].x - mb);
-                    l += w * ml[u].y;
-                    acc += w * o[u];
-                }
-            }
-            m = mb;
+            merge_batch8(m, l, acc, ml, o, c0, used, n);
         }
         red4[r * dpw + dd] = acc;
         if (dd == 0) red_ml[r] = make_float2(m, l);
     }
     __syncthreads();
     if (tid < dpw && dok) {
-        float M = red_ml[0].x;
-        for (int rr = 1; rr < used; ++rr) M = fmaxf(M, red_ml[rr].x);
-        floatx4 total{0.f, 0.f, 0.f, 0.f};
-        float l = 0.0f;
-        for (int rr = 0; rr < used; ++rr) {
-            const float2 ml = red_ml[rr];
-            const float f = expf(ml.x - M);
-            total += f * red4[rr * dpw + tid];
-            l += f * ml.y;
-        }
         reinterpret_cast<floatx4*>(a.out + static_cast<std::size_t>(i) * a.out_stride +
                                    static_cast<std::size_t>(h) * a.head_size)[d] =
-            total * (1.0f / l);
+            merge_combine(used, floatx4{0.f, 0.f, 0.f, 0.f},
+                          [&](int rr) { return red_ml[rr]; },
+                          [&](int rr) { return red4[rr * dpw + tid]; });
     }
 }
 
@@ -761,12 +736,7 @@ void launch_tile(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t st
     }
 }
 
-template <int G, int LPP, int F, bool ROPE>
-void launch_split(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t stream) {
-    const dim3 grid(s.n_heads / G, rows, a.splits);
-    hipLaunchKernelGGL((attn_split_kernel<G, LPP, F, ROPE>), grid, dim3(kThreads),
-                       split_lds(s, ROPE), stream, a);
-    if (a.splits == 1) return;  // one chunk per row: written directly
+void launch_merge(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t stream) {
     const int hs4 = s.head_size / 4;
     const int dpw = hs4 < kMergeDims ? hs4 : kMergeDims, groups = (hs4 + dpw - 1) / dpw;
     const std::size_t slots = kThreads / dpw;
@@ -774,15 +744,27 @@ void launch_split(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t s
                        (slots * dpw * 4 + 2 * slots) * sizeof(float), stream, a);
 }
 
+// merge false: the chunks are left for the caller to merge.
+template <int G, int LPP, int F, bool ROPE>
+void launch_split(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t stream,
+                  bool merge) {
+    const dim3 grid(s.n_heads / G, rows, a.splits);
+    hipLaunchKernelGGL((attn_split_kernel<G, LPP, F, ROPE>), grid, dim3(kThreads),
+                       split_lds(s, ROPE), stream, a);
+    if (a.splits == 1 || !merge) return;  // one chunk per row: written directly
+    launch_merge(s, a, rows, stream);
+}
+
 template <int G, bool ROPE = false>
-void launch_split_g(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t stream) {
+void launch_split_g(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t stream,
+                    bool merge = true) {
     switch (split_lanes(s) * 10 + split_f(s)) {
-        case 41: launch_split<G, 4, 1, ROPE>(s, a, rows, stream); break;
-        case 81: launch_split<G, 8, 1, ROPE>(s, a, rows, stream); break;
-        case 161: launch_split<G, 16, 1, ROPE>(s, a, rows, stream); break;
-        case 321: launch_split<G, 32, 1, ROPE>(s, a, rows, stream); break;
-        case 641: launch_split<G, 64, 1, ROPE>(s, a, rows, stream); break;
-        default: launch_split<G, 64, 2, ROPE>(s, a, rows, stream); break;
+        case 41: launch_split<G, 4, 1, ROPE>(s, a, rows, stream, merge); break;
+        case 81: launch_split<G, 8, 1, ROPE>(s, a, rows, stream, merge); break;
+        case 161: launch_split<G, 16, 1, ROPE>(s, a, rows, stream, merge); break;
+        case 321: launch_split<G, 32, 1, ROPE>(s, a, rows, stream, merge); break;
+        case 641: launch_split<G, 64, 1, ROPE>(s, a, rows, stream, merge); break;
+        default: launch_split<G, 64, 2, ROPE>(s, a, rows, stream, merge); break;
     }
 }
 
@@ -884,7 +866,7 @@ void run_attention(const AttnShape& s, int rows, const int* pos, const float* q,
 
 bool run_attention_rope(const AttnShape& s, const int* pos, const Summed& src, int dim,
                         int kv_dim, const float* cos_t, const float* sin_t, float* kc, float* vc,
-                        float* out, float* scratch, hipStream_t stream) {
+                        float* out, float* scratch, hipStream_t stream, SplitRow* defer) {
     if (resolve(kAttnAutomatic, 1, s) != kAttnSplit || split_lds(s, true) > kMaxLds) return false;
     if (src.n % 4 || src.mn % 4 || dim % 4 || kv_dim % 4) return false;
     if (!aligned16(src.slices == 1 ? src.c : src.partial) || (src.scale && !aligned16(src.scale)))
@@ -898,13 +880,26 @@ bool run_attention_rope(const AttnShape& s, const int* pos, const Summed& src, i
     a.sin_t = sin_t;
     a.kc_w = kc;
     a.vc_w = vc;
+    const bool hold = defer && a.splits > 1;
     switch (heads_per_block(s)) {
-        case 8: launch_split_g<8, true>(s, a, 1, stream); break;
-        case 4: launch_split_g<4, true>(s, a, 1, stream); break;
-        case 2: launch_split_g<2, true>(s, a, 1, stream); break;
-        default: launch_split_g<1, true>(s, a, 1, stream); break;
+        case 8: launch_split_g<8, true>(s, a, 1, stream, !hold); break;
+        case 4: launch_split_g<4, true>(s, a, 1, stream, !hold); break;
+        case 2: launch_split_g<2, true>(s, a, 1, stream, !hold); break;
+        default: launch_split_g<1, true>(s, a, 1, stream, !hold); break;
+    }
+    if (defer) {
+        *defer = SplitRow{};
+        if (hold) *defer = SplitRow{a.part_o, a.part_ml, out, pos, a.splits, s.n_heads, s.head_size};
     }
     return true;
+}
+
+void run_attention_merge(const AttnShape& s, const SplitRow& r, float* out, hipStream_t stream) {
+    AttnArgs a = base_args(s, 1, r.pos, nullptr, nullptr, nullptr, out);
+    a.splits = r.splits;
+    a.part_o = const_cast<float*>(r.o);
+    a.part_ml = const_cast<float2*>(r.ml);
+    launch_merge(s, a, 1, stream);
 }
 
 }  // namespace em

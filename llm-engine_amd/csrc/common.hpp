@@ -181,6 +181,73 @@ __device__ __forceinline__ floatx4 summed4(const Summed& s, int row, int col) {
 // expression every kernel that forms it uses, so they agree bit for bit.
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
+// Split attention (one workgroup per chunk of the context): at least
+// kSplitMinChunk positions per chunk, and a row of n_ctx positions over at
+// most `splits` chunks has ceil(n_ctx / split_chunk(n_ctx, splits)) of them
+// (cuda_attention.cu:25-31).
+constexpr int kSplitMinChunk = 64;
+__host__ __device__ __forceinline__ int split_chunk(int n_ctx, int splits) {
+    const int c = (n_ctx + splits - 1) / splits;
+    return c > kSplitMinChunk ? c : kSplitMinChunk;
+}
+
+// One decode row's split attention output before its merge. Chunk c of
+// head h leaves its max score and its sum of e^(score - max) in
+// ml[h * splits + c] and its unnormalised output in
+// o[(h * splits + c) * head_size, + head_size); a row whose positions fit
+// one chunk is written, normalised, to out[h * head_size + d] instead.
+// The row sits at position *pos, so n_ctx = *pos + 1.
+struct SplitRow {
+    const float* o;
+    const float2* ml;
+    const float* out;
+    const int* pos;
+    int splits, n_heads, head_size;
+};
+
+// The split merge (cuda_attention.cu:234-255: m = max m_c,
+// l = sum e^(m_c - m) l_c, out = sum e^(m_c - m) o_c / l), one batch of eight chunks into a running max m, sum l and output acc: chunk
+// u counts when c0 + u * stride < n. Every kernel that merges chunks runs
+// this and merge_combine, so they give the same bits.
+template <class T>
+__device__ __forceinline__ void merge_batch8(float& m, float& l, T& acc, const float2* ml,
+                                             const T* o, int c0, int stride, int n) {
+    float mb = m;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+        if (c0 + u * stride < n) mb = fmaxf(mb, ml[u].x);
+    // mb is finite: chunk c0 < n holds at least one position.
+    const float alpha = expf(m - mb);  // 0 while m = -inf
+    l *= alpha;
+    acc *= alpha;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        if (c0 + u * stride < n) {
+            const float w = expf(ml[u].x - mb);
+            l += w * ml[u].y;
+            acc += w * o[u];
+        }
+    }
+    m = mb;
+}
+
+// Slots 0 .. used - 1 of (max, sum) ml(r) and output acc(r), combined in
+// slot order: sum_r e^(m_r - M) acc_r / sum_r e^(m_r - M) l_r, M = max m_r.
+template <class T, class ML, class ACC>
+__device__ __forceinline__ T merge_combine(int used, T zero, ML ml, ACC acc) {
+    float M = ml(0).x;
+    for (int r = 1; r < used; ++r) M = fmaxf(M, ml(r).x);
+    T total = zero;
+    float l = 0.0f;
+    for (int r = 0; r < used; ++r) {
+        const float2 v = ml(r);
+        const float f = expf(v.x - M);
+        total += f * acc(r);
+        l += f * v.y;
+    }
+    return total * (1.0f / l);
+}
+
 // Tile of workgroup `id` of a 1-D grid. Workgroups are dispatched to the
 // eight XCDs in turn (id % 8), each XCD with its own L2. With xcd_order the
 // ids are renumbered so that each XCD receives a contiguous run of tiles,

@@ -110,7 +110,12 @@ struct GemvParams {
     int hidden;          // SWI: its gate | up split
     const float* ssq;    // NORM 2: sums of squares of A, one per 64 values
     int ssq_parts;       // NORM 2: their count, ceil(k / 64) <= kSsqParts
+    SplitRow att;        // merged source: the attention chunks A is merged from
 };
+
+// Where A comes from: read (kSrcA), or formed in the A staging from a
+// gate | up product (kSrcSwiGLU) or from split attention chunks (kSrcMerge).
+constexpr int kSrcA = 0, kSrcSwiGLU = 1, kSrcMerge = 2;
 
 // Slices a SwiGLU source may have: its values are loaded into registers.
 constexpr int kSwiSlices = 16;
@@ -124,12 +129,16 @@ constexpr int kSsqParts = 4 * kWave;
 // 64 values (p.ssq): each wave adds them with a fixed butterfly, so every
 // lane and workgroup gets the same bits without a barrier, and no
 // workgroup reads more of A than its own slice.
-// SWI (one row, at most 256 rows of k per workgroup): A is not read but
-// formed, A[j] = silu_mul(gate[j], up[j]) of a product given as a Summed
-// (p.gu, gate | up at p.hidden): the arithmetic of the forward pass's SwiGLU
-// kernel, so the result is the same as running that kernel first.
-template <class BT, int MM, int E, int L, int NORM, bool SWI = false>
+// SRC: formed sources take one row and at most 256 rows of k per
+// workgroup, one A value per thread. kSrcSwiGLU: A[j] = silu_mul(gate[j],
+// up[j]) of a product given as a Summed (p.gu, gate | up at p.hidden): the
+// arithmetic of the forward pass's SwiGLU kernel, so the result is the same
+// as running that kernel first. kSrcMerge: A[h * hs + d] is the merge of
+// head h's attention chunks (p.att, at most kMergeInGemv of them) in the
+// merge kernel's slots and order, so the result is the same as merging first.
+template <class BT, int MM, int E, int L, int NORM, int SRC = kSrcA>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
+    constexpr bool SWI = SRC == kSrcSwiGLU, MRG = SRC == kSrcMerge;
     using LT = Lane<BT, E>;
     using V = typename LT::V;
     constexpr int LPR = kThreads / E;  // lanes across one 256-column run
@@ -154,7 +163,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
     // of (k = tid, tid + 256, ...), loaded before the weight loads. A loop
     // of loads after them would wait for the whole weight stream at its
     // first s_waitcnt and then take one L2 round trip per step.
-    static_assert(NORM != 2 || (MM == 1 && !SWI), "producer sums of squares: one row");
+    static_assert(NORM != 2 || (MM == 1 && SRC == kSrcA), "producer sums of squares: one row");
     constexpr int NP = NORM != 1 ? 1 : MM == 1 ? 32 : MM == 2 ? 16 : MM <= 4 ? 4 : 2;
     // Loads are unconditional (addresses clamped into A; k >= 1 here) so
     // that no branch separates them; values past m or k are masked at use.
@@ -188,7 +197,23 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
     // weight loads so its wait does not include them.
     float a_reg[AREG];
     float sg[SWI ? kSwiSlices : 1], su[SWI ? kSwiSlices : 1];
-    if constexpr (SWI) {
+    float mo[MRG ? kMergeInGemv : 1], mout = 0.0f;
+    float2 mml[MRG ? kMergeInGemv : 1];
+    if constexpr (MRG) {
+        static_assert(MM == 1 && AREG == 1 && !NORM, "merged source: one row, one value per thread");
+        // This thread's column of every chunk its head may have (clamped
+        // past splits; only the row's chunks are used) and of out, which
+        // holds the row when it has one chunk: nothing waits for *pos.
+        const int col = min(p0 + tid % R, p.k - 1);
+        const int h = col / p.att.head_size, d = col - h * p.att.head_size;
+        mout = p.att.out[col];
+#pragma unroll
+        for (int c = 0; c < kMergeInGemv; ++c) {
+            const int b = h * p.att.splits + min(c, p.att.splits - 1);
+            mml[c] = p.att.ml[b];
+            mo[c] = p.att.o[static_cast<size_t>(b) * p.att.head_size + d];
+        }
+    } else if constexpr (SWI) {
         static_assert(MM == 1 && AREG == 1 && !NORM, "SwiGLU source: one row, one value per thread");
         // Gate and up of this thread's k index, every slice (clamped past
         // the last; only the first gu.slices are added).
@@ -261,6 +286,44 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
             }
         }
         a_reg[0] = (tid < R && p0 + tid % R < p.k) ? silu_mul(g, u) : 0.0f;
+    }
+    if constexpr (MRG) {
+        const int n_ctx = *p.att.pos + 1;
+        const int chunk = split_chunk(n_ctx, p.att.splits);
+        const int n = (n_ctx + chunk - 1) / chunk;
+        float v = mout;
+        float2 ml8[8];
+        float o8[8];
+        if (n > 1 && n <= 8) {
+            // One slot over chunks 0 .. n - 1.
+            float m = -INFINITY, l = 0.0f, acc = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                ml8[u] = mml[u];
+                o8[u] = mo[u];
+            }
+            merge_batch8(m, l, acc, ml8, o8, 0, 1, n);
+            const float2 s0 = make_float2(m, l);
+            v = merge_combine(1, 0.0f, [&](int) { return s0; }, [&](int) { return acc; });
+        } else if (n > 8) {
+            // Two slots: chunks 0, 2, 4, ... and 1, 3, 5, ...
+            float2 sm[2];
+            float sa[2];
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                float m = -INFINITY, l = 0.0f, acc = 0.0f;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    ml8[u] = mml[2 * u + r];
+                    o8[u] = mo[2 * u + r];
+                }
+                merge_batch8(m, l, acc, ml8, o8, r, 2, n);
+                sm[r] = make_float2(m, l);
+                sa[r] = acc;
+            }
+            v = merge_combine(2, 0.0f, [&](int r) { return sm[r]; }, [&](int r) { return sa[r]; });
+        }
+        a_reg[0] = (tid < R && p0 + tid % R < p.k) ? v : 0.0f;
     }
     if constexpr (NORM == 1) {
 #pragma unroll
@@ -514,12 +577,12 @@ int run_skinny_partials(const MatmulArgs& a, const float** partial) {
     return slices;
 }
 
-// x (k = hidden) = silu_mul of a Summed w13 product, times W (hidden x n),
-// one row: the forward pass's SwiGLU and w2 product in one GEMV.
-template <class BT>
-int run_skinny_swiglu_partials(const MatmulArgs& a, const Summed& gu, int hidden,
-                               const float** partial) {
-    if (a.m != 1 || gu.slices > kSwiSlices || a.rms_weight) return 0;
+namespace {
+
+// One row whose A the kernel forms (SRC), p carrying the source's fields:
+// the launch and its k slices, 0 if the shape has no 4- or 16-wide lanes.
+template <class BT, int SRC>
+int run_formed_partials(const MatmulArgs& a, GemvParams<BT> p, const float** partial) {
     const BT* B = static_cast<const BT*>(a.B);
     int E = 1;
     if (std::is_same<BT, int8_t>::value && a.n % 16 == 0 && aligned(B, 16)) {
@@ -533,7 +596,6 @@ int run_skinny_swiglu_partials(const MatmulArgs& a, const Summed& gu, int hidden
     while (E * L > kThreads) L /= 2;
     const int slices = ceil_div(a.k, E * L);
     const dim3 grid(ceil_div(a.n, kThreads), slices);
-    GemvParams<BT> p{};
     p.m = 1;
     p.n = a.n;
     p.k = a.k;
@@ -541,35 +603,35 @@ int run_skinny_swiglu_partials(const MatmulArgs& a, const Summed& gu, int hidden
     p.scale = a.scale;
     p.direct = slices == 1;
     p.accumulate = a.accumulate && p.direct;
-    p.out = p.direct ? a.C : scratch(kPartialFromPartial, static_cast<size_t>(slices) * a.n);
-    p.gu = gu;
-    p.hidden = hidden;
+    // A SwiGLU source reads the w13 GEMV's partials in slot 0.
+    p.out = p.direct ? a.C
+                     : scratch(SRC == kSrcSwiGLU ? kPartialFromPartial : kPartial,
+                               static_cast<size_t>(slices) * a.n);
     auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, a.stream, p); };
     if constexpr (std::is_same<BT, int8_t>::value) {
         if (E == 16) {
             switch (L) {
-                case 4: go(gemv_kernel<BT, 1, 16, 4, 0, true>); break;
-                case 8: go(gemv_kernel<BT, 1, 16, 8, 0, true>); break;
-                default: go(gemv_kernel<BT, 1, 16, 16, 0, true>); break;
+                case 4: go(gemv_kernel<BT, 1, 16, 4, 0, SRC>); break;
+                case 8: go(gemv_kernel<BT, 1, 16, 8, 0, SRC>); break;
+                default: go(gemv_kernel<BT, 1, 16, 16, 0, SRC>); break;
             }
             *partial = p.direct ? nullptr : p.out;
             return slices;
         }
     }
     switch (L) {
-        case 4: go(gemv_kernel<BT, 1, 4, 4, 0, true>); break;
-        case 8: go(gemv_kernel<BT, 1, 4, 8, 0, true>); break;
-        case 16: go(gemv_kernel<BT, 1, 4, 16, 0, true>); break;
-        default: go(gemv_kernel<BT, 1, 4, 32, 0, true>); break;
+        case 4: go(gemv_kernel<BT, 1, 4, 4, 0, SRC>); break;
+        case 8: go(gemv_kernel<BT, 1, 4, 8, 0, SRC>); break;
+        case 16: go(gemv_kernel<BT, 1, 4, 16, 0, SRC>); break;
+        default: go(gemv_kernel<BT, 1, 4, 32, 0, SRC>); break;
     }
     *partial = p.direct ? nullptr : p.out;
     return slices;
 }
 
+// The slice sum after a formed-source GEMV, as run_skinny's.
 template <class BT>
-int run_skinny_swiglu(const MatmulArgs& a, const Summed& gu, int hidden, float* ssq) {
-    const float* partial = nullptr;
-    const int slices = run_skinny_swiglu_partials<BT>(a, gu, hidden, &partial);
+int finish_formed(const MatmulArgs& a, int slices, const float* partial, float* ssq) {
     if (slices > 1)
         run_reduce_slices(1, a.n, slices, partial,
                           std::is_same<BT, int8_t>::value ? a.scale : nullptr, a.C,
@@ -577,8 +639,39 @@ int run_skinny_swiglu(const MatmulArgs& a, const Summed& gu, int hidden, float* 
     return slices;
 }
 
+}  // namespace
+
+// x (k = hidden) = silu_mul of a Summed w13 product, times W (hidden x n),
+// one row: the forward pass's SwiGLU and w2 product in one GEMV.
+template <class BT>
+int run_skinny_swiglu(const MatmulArgs& a, const Summed& gu, int hidden, float* ssq) {
+    if (a.m != 1 || gu.slices > kSwiSlices || a.rms_weight) return 0;
+    GemvParams<BT> p{};
+    p.gu = gu;
+    p.hidden = hidden;
+    const float* partial = nullptr;
+    const int slices = run_formed_partials<BT, kSrcSwiGLU>(a, p, &partial);
+    return finish_formed<BT>(a, slices, partial, ssq);
+}
+
+// Attention output (k = heads x head_size) merged from its chunks, times W,
+// one row: the merge kernel's work inside the wo GEMV.
+template <class BT>
+int run_skinny_merged(const MatmulArgs& a, const SplitRow& att, float* ssq) {
+    if (a.m != 1 || a.rms_weight || att.splits < 1 || att.splits > kMergeInGemv ||
+        static_cast<long long>(att.n_heads) * att.head_size != a.k)
+        return 0;
+    GemvParams<BT> p{};
+    p.att = att;
+    const float* partial = nullptr;
+    const int slices = run_formed_partials<BT, kSrcMerge>(a, p, &partial);
+    return finish_formed<BT>(a, slices, partial, ssq);
+}
+
 template int run_skinny_swiglu<float>(const MatmulArgs&, const Summed&, int, float*);
 template int run_skinny_swiglu<int8_t>(const MatmulArgs&, const Summed&, int, float*);
+template int run_skinny_merged<float>(const MatmulArgs&, const SplitRow&, float*);
+template int run_skinny_merged<int8_t>(const MatmulArgs&, const SplitRow&, float*);
 
 template <class BT>
 void run_skinny(const MatmulArgs& a) {

@@ -214,6 +214,7 @@ private:
     Summed project_summed(int n, const float* in, const Proj& w, float* out, const float* rms,
                           const float* ssq);
     bool residual(int n, const float* in, const Proj& w);
+    bool residual_merged(const SplitRow& att, const Proj& w);
     bool swiglu_w2(const Summed& gu, const Proj& w2, bool* wrote_ssq);
     void reserve_rows(std::size_t n);
     void enqueue(int n);
@@ -389,6 +390,22 @@ bool Model::residual(int n, const float* in, const Proj& w) {
     return slices > 1;
 }
 
+// x += att W for one decode row whose attention chunks are not merged yet:
+// the GEMV merges them in its A staging (run_skinny_merged), one launch
+// fewer; for a shape it does not take, the merge kernel writes att first.
+bool Model::residual_merged(const SplitRow& att, const Proj& w) {
+    const MatmulArgs a = gemv_args(1, nullptr, w, x_.p, nullptr, true, nullptr);
+    float* ssq = use_ssq_ ? ssq_.p : nullptr;
+    const int slices = q8_ ? run_skinny_merged<int8_t>(a, att, ssq)
+                           : run_skinny_merged<float>(a, att, ssq);
+    if (slices) {
+        check(hipGetLastError(), "launch");
+        return ssq && slices > 1;
+    }
+    run_attention_merge(shape_, att, att_.p, stream_);
+    return residual(1, att_.p, w);
+}
+
 // One decode row: x += silu_mul(gate, up) W2 with the SwiGLU formed inside
 // the w2 GEMV (run_skinny_swiglu) rather than by swiglu_kernel first: one
 // launch fewer, the same values. False if the GEMV does not take the shape.
@@ -435,17 +452,19 @@ void Model::enqueue(int n) {
     for (LayerDev& L : layers_) {
         const Summed qkv = project_summed(n, x_.p, L.wqkv, qkv_.p, L.rms_att.p,
                                           have_ssq ? ssq_.p : nullptr);
-        // One row: RoPE and the cache write inside the attention launch.
+        // One row: RoPE and the cache write inside the attention launch,
+        // and the chunks' merge inside the wo GEMV.
+        SplitRow chunks{};
         if (!(n == 1 && run_attention_rope(shape_, feed_dev_.p, qkv, D, KV, rope_cos_.p,
                                            rope_sin_.p, L.kcache.p, L.vcache.p, att_.p,
-                                           attn_scratch_.p, stream_))) {
+                                           attn_scratch_.p, stream_, &chunks))) {
             hipLaunchKernelGGL(rope_cache_kernel, dim3(ceil_div(rope_threads, kThreads), n),
                                dim3(kThreads), 0, stream_, qkv, qkv_cols, D, KV, hs, feed_dev_.p,
                                rope_cos_.p, rope_sin_.p, qkv_.p, L.kcache.p, L.vcache.p);
             run_attention(shape_, n, feed_dev_.p, qkv_.p, L.kcache.p, L.vcache.p, att_.p,
                           attn_scratch_.p, kAttnAutomatic, stream_);
         }
-        have_ssq = residual(n, att_.p, L.wo);
+        have_ssq = chunks.o ? residual_merged(chunks, L.wo) : residual(n, att_.p, L.wo);
         const Summed gu = project_summed(n, x_.p, L.w13, gu_.p, L.rms_ffn.p,
                                          have_ssq ? ssq_.p : nullptr);
         if (!(n == 1 && swiglu_w2(gu, L.w2, &have_ssq))) {
