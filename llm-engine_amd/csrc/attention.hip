@@ -122,6 +122,7 @@ int resolve(int kernel, std::size_t rows, const AttnShape& s) {
 
 struct AttnArgs {
     int n_heads, head_size, group, seq_len, splits, chunk_cap, rows;
+    int merge_from;  // the merge kernel takes rows of at least this many chunks (>= 2)
     int q_stride, kv_stride, out_stride;
     const int* pos;
     const float* q;
@@ -413,7 +414,7 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
     const int n_ctx = *a.pos + i + 1;
     const int chunk = chunk_size(n_ctx, a.splits);
     const int n = (n_ctx + chunk - 1) / chunk;
-    if (n == 1) return;  // written by the split kernel
+    if (n < a.merge_from) return;  // one chunk: written by the split kernel; few: by their consumer
     const std::size_t b = (static_cast<std::size_t>(i) * a.n_heads + h) * a.splits;
     const int tid = threadIdx.x;
     const int slots = kThreads / dpw, r = tid / dpw, dd = tid % dpw, d = d0 + dd;
@@ -744,27 +745,26 @@ void launch_merge(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t s
                        (slots * dpw * 4 + 2 * slots) * sizeof(float), stream, a);
 }
 
-// merge false: the chunks are left for the caller to merge.
+// Rows of fewer than a.merge_from chunks are left for the caller to merge;
+// no merge launches when no row can have that many.
 template <int G, int LPP, int F, bool ROPE>
-void launch_split(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t stream,
-                  bool merge) {
+void launch_split(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t stream) {
     const dim3 grid(s.n_heads / G, rows, a.splits);
     hipLaunchKernelGGL((attn_split_kernel<G, LPP, F, ROPE>), grid, dim3(kThreads),
                        split_lds(s, ROPE), stream, a);
-    if (a.splits == 1 || !merge) return;  // one chunk per row: written directly
+    if (a.splits < a.merge_from) return;  // e.g. one chunk per row: written directly
     launch_merge(s, a, rows, stream);
 }
 
 template <int G, bool ROPE = false>
-void launch_split_g(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t stream,
-                    bool merge = true) {
+void launch_split_g(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t stream) {
     switch (split_lanes(s) * 10 + split_f(s)) {
-        case 41: launch_split<G, 4, 1, ROPE>(s, a, rows, stream, merge); break;
-        case 81: launch_split<G, 8, 1, ROPE>(s, a, rows, stream, merge); break;
-        case 161: launch_split<G, 16, 1, ROPE>(s, a, rows, stream, merge); break;
-        case 321: launch_split<G, 32, 1, ROPE>(s, a, rows, stream, merge); break;
-        case 641: launch_split<G, 64, 1, ROPE>(s, a, rows, stream, merge); break;
-        default: launch_split<G, 64, 2, ROPE>(s, a, rows, stream, merge); break;
+        case 41: launch_split<G, 4, 1, ROPE>(s, a, rows, stream); break;
+        case 81: launch_split<G, 8, 1, ROPE>(s, a, rows, stream); break;
+        case 161: launch_split<G, 16, 1, ROPE>(s, a, rows, stream); break;
+        case 321: launch_split<G, 32, 1, ROPE>(s, a, rows, stream); break;
+        case 641: launch_split<G, 64, 1, ROPE>(s, a, rows, stream); break;
+        default: launch_split<G, 64, 2, ROPE>(s, a, rows, stream); break;
     }
 }
 
@@ -824,6 +824,7 @@ AttnArgs base_args(const AttnShape& s, int rows, const int* pos, const float* q,
     a.vc = vc;
     a.out = out;
     a.rows = rows;
+    a.merge_from = 2;
     return a;
 }
 
@@ -880,12 +881,15 @@ bool run_attention_rope(const AttnShape& s, const int* pos, const Summed& src, i
     a.sin_t = sin_t;
     a.kc_w = kc;
     a.vc_w = vc;
+    // Deferred: rows of up to kMergeInGemv chunks are merged by the consumer,
+    // longer ones (a shape with more splits) by the merge kernel, into out.
     const bool hold = defer && a.splits > 1;
+    if (hold) a.merge_from = kMergeInGemv + 1;
     switch (heads_per_block(s)) {
-        case 8: launch_split_g<8, true>(s, a, 1, stream, !hold); break;
-        case 4: launch_split_g<4, true>(s, a, 1, stream, !hold); break;
-        case 2: launch_split_g<2, true>(s, a, 1, stream, !hold); break;
-        default: launch_split_g<1, true>(s, a, 1, stream, !hold); break;
+        case 8: launch_split_g<8, true>(s, a, 1, stream); break;
+        case 4: launch_split_g<4, true>(s, a, 1, stream); break;
+        case 2: launch_split_g<2, true>(s, a, 1, stream); break;
+        default: launch_split_g<1, true>(s, a, 1, stream); break;
     }
     if (defer) {
         *defer = SplitRow{};

@@ -134,8 +134,9 @@ constexpr int kSsqParts = 4 * kWave;
 // up[j]) of a product given as a Summed (p.gu, gate | up at p.hidden): the
 // arithmetic of the forward pass's SwiGLU kernel, so the result is the same
 // as running that kernel first. kSrcMerge: A[h * hs + d] is the merge of
-// head h's attention chunks (p.att, at most kMergeInGemv of them) in the
-// merge kernel's slots and order, so the result is the same as merging first.
+// head h's attention chunks (p.att) in the merge kernel's slots and order,
+// so the result is the same as merging first; a row of one chunk, or of
+// more than kMergeInGemv, is read from p.att.out.
 template <class BT, int MM, int E, int L, int NORM, int SRC = kSrcA>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
     constexpr bool SWI = SRC == kSrcSwiGLU, MRG = SRC == kSrcMerge;
@@ -201,9 +202,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
     float2 mml[MRG ? kMergeInGemv : 1];
     if constexpr (MRG) {
         static_assert(MM == 1 && AREG == 1 && !NORM, "merged source: one row, one value per thread");
-        // This thread's column of every chunk its head may have (clamped
-        // past splits; only the row's chunks are used) and of out, which
-        // holds the row when it has one chunk: nothing waits for *pos.
+        // This thread's column of the first kMergeInGemv chunks its head
+        // may have (clamped past splits; only the row's chunks are used) and
+        // of out, which holds the row when it has one chunk or more than
+        // kMergeInGemv (merged by the merge kernel): nothing waits for *pos.
         const int col = min(p0 + tid % R, p.k - 1);
         const int h = col / p.att.head_size, d = col - h * p.att.head_size;
         mout = p.att.out[col];
@@ -305,7 +307,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
             merge_batch8(m, l, acc, ml8, o8, 0, 1, n);
             const float2 s0 = make_float2(m, l);
             v = merge_combine(1, 0.0f, [&](int) { return s0; }, [&](int) { return acc; });
-        } else if (n > 8) {
+        } else if (n > 8 && n <= kMergeInGemv) {
             // Two slots: chunks 0, 2, 4, ... and 1, 3, 5, ...
             float2 sm[2];
             float sa[2];
@@ -658,7 +660,7 @@ int run_skinny_swiglu(const MatmulArgs& a, const Summed& gu, int hidden, float* 
 // one row: the merge kernel's work inside the wo GEMV.
 template <class BT>
 int run_skinny_merged(const MatmulArgs& a, const SplitRow& att, float* ssq) {
-    if (a.m != 1 || a.rms_weight || att.splits < 1 || att.splits > kMergeInGemv ||
+    if (a.m != 1 || a.rms_weight || att.splits < 1 ||
         static_cast<long long>(att.n_heads) * att.head_size != a.k)
         return 0;
     GemvParams<BT> p{};

@@ -76,9 +76,10 @@ int run_skinny_partials(const MatmulArgs& a, const float** partial);
 template <class BT>
 int run_skinny_swiglu(const MatmulArgs& a, const Summed& gu, int hidden, float* ssq = nullptr);
 // One row of attention output x B with A merged inside the GEMV's A
-// staging from the split chunks att (at most kMergeInGemv per row, k =
-// heads x head_size), as the merge kernel merges them: the same bits as
-// run_attention_merge followed by run_skinny. Returns the k slices and
+// staging from the split chunks att (k = heads x head_size) when the row
+// has 2 .. kMergeInGemv of them, as the merge kernel merges them, and read
+// from att.out otherwise: the same bits as run_attention_merge followed by
+// run_skinny. Returns the k slices and
 // writes ssq as run_skinny_swiglu does; 0 (nothing launched) for a shape
 // it does not take.
 constexpr int kMergeInGemv = 16;
@@ -159,10 +160,11 @@ void run_attention(const AttnShape& s, int rows, const int* pos, const float* q,
 // k and v are written to the caches at *pos, and out receives attention over
 // positions 0 .. *pos. Scratch as run_attention's for one row. False
 // (nothing launched) for a shape or alignment it does not take.
-// With defer, a row split over chunks is not merged: *defer describes the
-// chunks (and `out`, which holds the row when its context fits one chunk)
-// for the consumer to merge, run_skinny_merged or run_attention_merge;
-// defer->o is null when the shape has one chunk per row and out is written.
+// With defer, a row split over up to kMergeInGemv chunks is not merged:
+// *defer describes the chunks for the consumer to merge, run_skinny_merged
+// or run_attention_merge. `out` holds the row when it has one chunk, or
+// (a shape with more splits) more than kMergeInGemv, merged by the merge
+// kernel. defer->o is null when the shape has one chunk per row.
 bool run_attention_rope(const AttnShape& s, const int* pos, const Summed& src, int dim,
                         int kv_dim, const float* cos_t, const float* sin_t, float* kc, float* vc,
                         float* out, float* scratch, hipStream_t stream,

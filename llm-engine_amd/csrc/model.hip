@@ -25,6 +25,7 @@
 // Everything runs on one stream the model owns, at default priority.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <stdexcept>
 #include <string>
@@ -237,6 +238,9 @@ private:
     // One-token steps: sums of squares of x per 64 values, left by the
     // kernel that last wrote x for the next norm GEMV (dim % 64 == 0).
     bool use_ssq_ = false;
+    // EM_DECODE_MERGE_KERNEL=1 at creation: one-row steps merge the
+    // attention chunks with the merge kernel, not in the wo GEMV (tests).
+    bool merge_kernel_ = false;
     Buf<float> ssq_;
 
     Pinned<int> feed_host_;  // [pos, tokens...]
@@ -292,6 +296,8 @@ Model::Model(const em_model_config& c, const float* emb, const em_layer_weights*
     feed_dev_.alloc(c.seq_len + 1);
     use_ssq_ = D % kSsqChunk == 0 && D / kSsqChunk <= 256;
     if (use_ssq_) ssq_.alloc(D / kSsqChunk);
+    const char* mk = std::getenv("EM_DECODE_MERGE_KERNEL");
+    merge_kernel_ = mk && std::atoi(mk) != 0;
     check(hipStreamSynchronize(stream_), "load weights");
     reserve_rows(1);
 }
@@ -457,7 +463,8 @@ void Model::enqueue(int n) {
         SplitRow chunks{};
         if (!(n == 1 && run_attention_rope(shape_, feed_dev_.p, qkv, D, KV, rope_cos_.p,
                                            rope_sin_.p, L.kcache.p, L.vcache.p, att_.p,
-                                           attn_scratch_.p, stream_, &chunks))) {
+                                           attn_scratch_.p, stream_,
+                                           merge_kernel_ ? nullptr : &chunks))) {
             hipLaunchKernelGGL(rope_cache_kernel, dim3(ceil_div(rope_threads, kThreads), n),
                                dim3(kThreads), 0, stream_, qkv, qkv_cols, D, KV, hs, feed_dev_.p,
                                rope_cos_.p, rope_sin_.p, qkv_.p, L.kcache.p, L.vcache.p);

@@ -122,27 +122,29 @@ def test_norm_from_producer_sums_of_squares(tmp_path, dim, hidden, heads, kv_hea
     gpu.close()
 
 
+@pytest.mark.parametrize("seq_len", [1024, 2048])
 @pytest.mark.parametrize("dim,hidden,heads,kv_heads,wtype",
                          [(256, 688, 4, 2, "q8"), (256, 688, 2, 2, "f32")],
                          ids=["hs64_gqa_q8", "hs128_f32"])
-def test_decode_merge_inside_wo_gemv(tmp_path, dim, hidden, heads, kv_heads, wtype):
+def test_decode_merge_inside_wo_gemv(tmp_path, monkeypatch, dim, hidden, heads, kv_heads,
+                                     wtype, seq_len):
     # One-token steps leave the split attention's chunks unmerged, and the wo
-    # GEMV merges them as it stages its A when a row has at most 16 chunks
-    # (seq_len <= 1024); with more (seq_len 2048) the merge kernel writes
-    # the attention output first. Up to position 1023 both models cut the
-    # context into the same 64-position chunks and merge them in the same
-    # slots and order, so every decode's logits must be the same bits. The
-    # decodes cover one chunk (the split kernel writes the row itself), a
-    # second chunk from position 64, one slot up to 8 chunks, two from 9
-    # (position 512) and the full 16 (from 960); each against the CPU
-    # Transformer too, greedy token equal, within the reference's 1e-4
-    # taken relative to the largest logit (~18 here; the reference's fixture
-    # logits are of order 1). The 3e-5 of the short-context test above is
-    # too tight over hundreds of positions: at position 55, where both
-    # models run the unchanged one-chunk path, fp32 summation order alone
-    # measured 3.7e-5.
+    # GEMV merges them as it stages its A when a row has 2 to 16 chunks of
+    # 64 positions; a row of more (seq_len 2048 allows 32) is merged by the
+    # merge kernel, and the GEMV reads its output. A second model created
+    # with EM_DECODE_MERGE_KERNEL=1 merges every row with the merge kernel
+    # first. Both merge in the same slots and order, so every decode's
+    # logits must be the same bits. The decodes cover one chunk (the split
+    # kernel writes the row itself), a second chunk from position 64, one
+    # slot up to 8 chunks, two from 9 (position 512), 16 from 960 and, at
+    # seq_len 2048, 17 from 1024; each against the CPU Transformer too,
+    # greedy token equal, within the reference's 1e-4 taken relative to the
+    # largest logit (~18 here; the reference's fixture logits are of order
+    # 1). The 3e-5 of the short-context test above is too tight over
+    # hundreds of positions: at position 55, where both models run the
+    # one-chunk path, fp32 summation order alone measured 3.7e-5.
     m = e2e_model.fixture_model(heads, kv_heads, False, seed=dim + 7 * heads, dim=dim,
-                                hidden=hidden, vocab=300, seq_len=1024)
+                                hidden=hidden, vocab=300, seq_len=seq_len)
     path = str(tmp_path / "model.bin")
     e2e_model.write_raw(path, m)
     ck = oracle.RefCheckpoint(lib, path)
@@ -150,18 +152,21 @@ def test_decode_merge_inside_wo_gemv(tmp_path, dim, hidden, heads, kv_heads, wty
     w = ck.weights()
     cpu = oracle.RefTransformer(lib, ck, q8)
     fused = em.Model(ck.config, w, q8=q8)
-    merged_first = em.Model(dict(ck.config, seq_len=2048), w, q8=q8)
+    monkeypatch.setenv("EM_DECODE_MERGE_KERNEL", "1")
+    merged_first = em.Model(ck.config, w, q8=q8)
+    monkeypatch.delenv("EM_DECODE_MERGE_KERNEL")
     V = ck.config["vocab_size"]
-    tokens = [(p * 13 + 7) % V for p in range(1024)]
+    tokens = [(p * 13 + 7) % V for p in range(seq_len)]
     pos, worst = 0, 0.0
-    for prefill_to, decode_to in ((40, 80), (500, 540), (1000, 1024)):
+    for prefill_to, decode_to in ((40, 80), (500, 540), (1000, min(1040, seq_len))):
         part = tokens[pos:prefill_to]
-        print(f"merge {wtype} heads {heads}: prefill {pos}..{prefill_to}", flush=True)
+        print(f"merge {wtype} heads {heads} seq_len {seq_len}: prefill {pos}..{prefill_to}",
+              flush=True)
         a, b = fused.forward(part, pos), merged_first.forward(part, pos)
         assert np.array_equal(a, b), f"prefill to {prefill_to}"
         cpu.run(part, pos)
         for pos in range(prefill_to, decode_to):
-            print(f"merge {wtype} heads {heads}: decode {pos}", flush=True)
+            print(f"merge {wtype} heads {heads} seq_len {seq_len}: decode {pos}", flush=True)
             a, b = fused.forward(tokens[pos], pos), merged_first.forward(tokens[pos], pos)
             assert np.array_equal(a, b), f"decode at {pos}: max diff {np.abs(a - b).max()}"
             c = cpu.run([tokens[pos]], pos, True)
