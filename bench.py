@@ -45,7 +45,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 FP32_MFMA_PEAK_TFLOPS = 157.3
 BF16_MFMA_PEAK_TFLOPS = 2516.6   # MI355X dense bf16 (no sparsity)
-# int8 B at m > 8 runs on bf16 MFMA with A split exactly into three bf16
+# int8 B above 8 rows (and at 2-8 rows by a shape rule) runs on bf16 MFMA with A split exactly into three bf16
 # terms: three MFMA products per fp32 multiply-add, so its compute roof in
 # fp32-equivalent flops is a third of the bf16 peak.
 EXACT_SPLIT_PEAK_TFLOPS = BF16_MFMA_PEAK_TFLOPS / 3
@@ -415,7 +415,7 @@ def profile_gemm_pass(em, torch, N: int = 4096, reps: int = 5) -> dict:
 
 def profile_split_pass(em, torch, m: int = 512, reps: int = 20) -> dict:
     """Eager int8 products at m rows over the rotating 4096^2 pool with the
-    `automatic` kernel (exact-split bf16 above 8 rows), for counter passes."""
+    `automatic` kernel (exact-split bf16 at these sizes), for counter passes."""
     per_copy = DIM * DIM
     copies = -(-POOL_MIN_BYTES // per_copy)
     pool = Pool(em, torch, True, DIM, DIM, copies, 1000)

@@ -87,12 +87,7 @@ int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, co
         a.accumulate = accumulate != 0;
         a.rms_weight = rms_weight;
         a.stream = s;
-        static const std::size_t split_min_rows = [] {
-            const char* v = std::getenv("EM_SPLIT_MIN_ROWS");  // tuning sweeps
-            const int x = v ? std::atoi(v) : 0;
-            return static_cast<std::size_t>(x > 8 ? x : 9);
-        }();
-        if (std::is_same<BT, int8_t>::value && automatic && m >= split_min_rows &&
+        if (std::is_same<BT, int8_t>::value && automatic && split_bf16_preferred(a.m, a.n, a.k) &&
             split_bf16_supports(a)) {
             run_split_bf16(a);  // fuses the norm
             hip_check(hipGetLastError(), "launch");

@@ -104,6 +104,10 @@ void run_naive(const MatmulArgs& a);
 // and scales.
 bool split_bf16_supports(const MatmulArgs& a);
 void run_split_bf16(const MatmulArgs& a);
+// True if automatic sends an int8 product of m rows (k x n weights) to the
+// exact-split kernel rather than the GEMV. EM_SPLIT_MIN_ROWS (2 or more)
+// replaces the rule by a row threshold, for sweeps.
+bool split_bf16_preferred(int m, int n, int k);
 
 // True if run_tiled_split can take this shape (vector loads of B rows).
 template <class BT>

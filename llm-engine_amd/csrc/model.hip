@@ -364,7 +364,7 @@ MatmulArgs Model::gemv_args(int n, const float* in, const Proj& w, float* out, c
 Summed Model::project_summed(int n, const float* in, const Proj& w, float* out,
                              const float* rms, const float* ssq) {
     Summed s{out, nullptr, nullptr, 1, w.cols, static_cast<std::size_t>(n) * w.cols};
-    if (n > 8) {
+    if (n > 8 || (q8_ && split_bf16_preferred(n, w.cols, w.rows))) {
         project(n, in, w, out, rms, false);
         return s;
     }

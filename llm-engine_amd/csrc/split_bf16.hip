@@ -1,5 +1,6 @@
 // int8-weight products on bf16 matrix cores with fp32 results: what
-// GpuKernel::automatic runs for int8 B at m > 8
+// GpuKernel::automatic runs for int8 B above 8 rows, and for fewer rows
+// where split_bf16_preferred says it beats the GEMV
 // (reference: tiled_split / tiled, /root/reference/src/cuda_matmul.cu:49-125,
 // 350-363; CPU pack_b dequantisation, matmul.cpp:73-90).
 //
@@ -423,6 +424,27 @@ void launch(const SbParams& p, int blocks, bool raw, hipStream_t s) {
 bool split_bf16_supports(const MatmulArgs& a) {
     return a.n % 16 == 0 && reinterpret_cast<uintptr_t>(a.B) % 16 == 0 &&
            reinterpret_cast<uintptr_t>(a.scale) % 16 == 0;
+}
+
+// The GEMV's cost grows with m (its multiply-adds, and from 5 rows an
+// 8-row kernel whose slices are half as deep), while this kernel pays for a
+// whole 16-row block at any m. Measured per call in HIP graphs, GEMV against
+// exact-split (us):
+//   4096 x 4096:   m 2  7.5 /  9.6, m 4  9.1 /  9.6, m 5 11.7 /  9.7, m 8 12.5 / 10.0
+//   4096 x 11008:  m 2 12.9 / 13.8, m 3 15.6 / 14.6, m 5 27.7 / 14.2, m 8 31.6 / 14.5
+//   11008 x 4096:  m 2 12.9 / 14.4, m 3 15.3 / 14.4, m 5 25.1 / 14.5, m 8 28.2 / 14.9
+//   4096 x 32000:  m 2 27.6 / 26.2, m 3 32.4 / 26.0, m 5 59.6 / 26.3, m 8 67.3 / 26.7
+// So: from 5 rows always; from 3 rows for 2^25 weights or more; from 2 rows
+// for 2^26 or more.
+bool split_bf16_preferred(int m, int n, int k) {
+    static const int forced = [] {
+        const char* v = std::getenv("EM_SPLIT_MIN_ROWS");  // tuning sweeps
+        const int x = v ? std::atoi(v) : 0;
+        return x >= 2 ? x : 0;
+    }();
+    if (forced) return m >= forced;
+    const long long w = static_cast<long long>(n) * k;
+    return m >= 5 || (m >= 3 && w >= (1LL << 25)) || (m >= 2 && w >= (1LL << 26));
 }
 
 void run_split_bf16(const MatmulArgs& a) {

@@ -328,7 +328,7 @@ SPLIT_SHAPES = [(9, 300, 32), (12, 4096, 4096), (24, 4096, 4096), (64, 4096, 409
 
 @pytest.mark.parametrize("shape", SPLIT_SHAPES, ids=lambda s: "x".join(map(str, s)))
 def test_exact_split_tighter_than_fp32_tolerance(shape):
-    # automatic sends int8 B at m > 8 to the exact-split bf16 kernel: with A
+    # automatic sends int8 B above 8 rows to the exact-split bf16 kernel: with A
     # split exactly into three bf16 terms, its only error is fp32 summation
     # order, so it must sit far inside the north star's 1e-4 * sum|a||w|.
     # A spans 1e-20 .. 1e20 within each row, which block-scaled (shared
