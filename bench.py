@@ -45,9 +45,10 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 FP32_MFMA_PEAK_TFLOPS = 157.3
 BF16_MFMA_PEAK_TFLOPS = 2516.6   # MI355X dense bf16 (no sparsity)
-# int8 B above 8 rows (and at 2-8 rows by a shape rule) runs on bf16 MFMA with A split exactly into three bf16
-# terms: three MFMA products per fp32 multiply-add, so its compute roof in
-# fp32-equivalent flops is a third of the bf16 peak.
+# int8 B above 8 rows (and at 2-8 rows by a shape rule) runs on bf16 MFMA
+# with A split exactly into three bf16 terms: three MFMA products per fp32
+# multiply-add, so its compute roof in fp32-equivalent flops is a third of
+# the bf16 peak.
 EXACT_SPLIT_PEAK_TFLOPS = BF16_MFMA_PEAK_TFLOPS / 3
 
 
