@@ -147,9 +147,10 @@ private:
 
 // cuda_matmul.h:66-72. The values are the C ABI's EM_KERNEL_* codes.
 enum class GpuKernel {
-    automatic = EM_KERNEL_AUTOMATIC,      // fp32: skinny for m <= 8, else tiled_split (tiled if B is
-                                          // unaligned); int8: skinny for 1 row and for 2-4 rows of
-                                          // small weights, else exact-split bf16 MFMA
+    automatic = EM_KERNEL_AUTOMATIC,      // fp32: skinny for m <= 8 (m <= 3 for 2^25 weights or
+                                          // more), else tiled_split (tiled if B is unaligned); int8:
+                                          // skinny for 1 row and for 2-4 rows of small weights,
+                                          // else exact-split bf16 MFMA
     naive = EM_KERNEL_NAIVE,              // one thread per element of C; the reference kernel
     tiled = EM_KERNEL_TILED,              // LDS-tiled fp32 MFMA, 128 x 128 tiles
     tiled_split = EM_KERNEL_TILED_SPLIT,  // MFMA on 16/32-row tiles, B streamed once, k split

@@ -37,9 +37,10 @@ extern "C" {
 #define EM_ERANGE 4  /* a token or position outside the model's range (std::out_of_range) */
 
 /* Kernel choice; replaces enum class GpuKernel, cuda_matmul.h:61-67. */
-#define EM_KERNEL_AUTOMATIC 0   /* fp32 B: skinny for m <= 8, else tiled_split (tiled if B is
-                                   unaligned); int8 B: skinny for 1 row, and for 2-4 rows of
-                                   small weights, else the exact-split bf16 MFMA kernel */
+#define EM_KERNEL_AUTOMATIC 0   /* fp32 B: skinny for m <= 8 (m <= 3 for 2^25 weights or more),
+                                   else tiled_split (tiled if B is unaligned); int8 B: skinny
+                                   for 1 row, and for 2-4 rows of small weights, else the
+                                   exact-split bf16 MFMA kernel */
 #define EM_KERNEL_NAIVE 1       /* one thread per element of C; the reference kernel */
 #define EM_KERNEL_TILED 2       /* LDS-tiled fp32 MFMA GEMM, 128 x 128 tiles */
 #define EM_KERNEL_TILED_SPLIT 3 /* MFMA over 16/32-row tiles, B streamed from HBM/L2, k split */

@@ -52,8 +52,12 @@ int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, co
     // gfx950 tiled_split measured as fast or faster up to m = 4096 (within
     // 2 % for fp32 at 4096^3). int8 B goes to the exact-split bf16 MFMA
     // kernel instead (split_bf16.hip: at 4096^2, 1.1x faster than
-    // tiled_split at m = 9-16 and 1.3-2.6x from m = 32 to 512). tiled takes
-    // what B's width or alignment rules out.
+    // tiled_split at m = 9-16 and 1.3-2.6x from m = 32 to 512), and so do
+    // int8 products of fewer rows where it beats the GEMV
+    // (split_bf16_preferred). fp32 B of 2^25 values or more takes tiled_split
+    // from 4 rows (4096 x 11008: 35.9 against 38.4 us at m = 4, 36.5
+    // against 41.8 at m = 8; at 4096^2 the GEMV stays ahead, 18.1 against
+    // 19.2 at m = 8). tiled takes what B's width or alignment rules out.
     const bool automatic = kernel == EM_KERNEL_AUTOMATIC;
     if (automatic) kernel = m <= 8 ? EM_KERNEL_SKINNY : EM_KERNEL_TILED_SPLIT;
     if (kernel == EM_KERNEL_SKINNY && m > 8)
@@ -93,6 +97,10 @@ int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, co
             hip_check(hipGetLastError(), "launch");
             return EM_OK;
         }
+        if (!std::is_same<BT, int8_t>::value && automatic && m >= 4 &&
+            static_cast<long long>(n) * static_cast<long long>(k) >= (1LL << 25) &&
+            tiled_split_supports<BT>(a))
+            kernel = EM_KERNEL_TILED_SPLIT;
         if (rms_weight && kernel != EM_KERNEL_SKINNY) {
             float* normed = scratch(kNorm, m * k);
             run_rmsnorm_rows(a.m, a.k, A, rms_weight, normed, s);
