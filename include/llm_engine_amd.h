@@ -119,7 +119,7 @@ typedef struct {
 } em_attention_shape;
 
 /* Replaces enum class AttentionKernel, cuda_attention.h:15-19. */
-#define EM_ATTN_AUTOMATIC 0    /* split for up to 8 rows; more rows: 16-row fp32 MFMA tiles
+#define EM_ATTN_AUTOMATIC 0    /* split for up to 12 rows; more rows: 16-row fp32 MFMA tiles
                                   (head_size a multiple of 16, at most 128), else one chunk
                                   per row, no merge */
 #define EM_ATTN_SINGLE_BLOCK 1 /* one workgroup per (head, row), scores in LDS */

@@ -24,7 +24,7 @@
 //    measured slower than a second launch, and the fixed merge order keeps
 //    results bit-identical across calls. A context that fits one chunk is
 //    normalised and written by the first kernel; the merge kernel then exits.
-//    With more than 8 rows (prefill), automatic runs the same kernel with
+//    With more than 12 rows (prefill), automatic runs the same kernel with
 //    one chunk per row: the whole context in rounds, no merge.
 //  * single_block (on request): workgroup (head, row) holds the query and
 //    the scores of the whole context in LDS; any head size.
@@ -42,7 +42,7 @@ namespace {
 
 constexpr int kMinChunk = kSplitMinChunk;  // positions per split workgroup, at least
 constexpr int kMaxSplits = 256;         // chunks per (row, head group), at most
-constexpr std::size_t kSplitMaxRows = 8;   // automatic: split up to this many rows
+constexpr std::size_t kSplitMaxRows = 12;  // automatic: split up to this many rows
 constexpr std::size_t kMaxLds = 64 * 1024;  // dynamic LDS per workgroup
 
 int split_count(int seq_len) {
@@ -100,8 +100,13 @@ SplitScratch split_scratch(const AttnShape& s, std::size_t rows) {
     return l;
 }
 
-// automatic: the split kernel with chunks across workgroups for up to 8 rows.
-// Beyond, the tile kernel (16 query rows per wave on fp32 MFMA, each key and
+// automatic: the split kernel with chunks across workgroups for up to 12
+// rows. Its cost grows with the rows (each reads its chunks' keys and
+// values), while a tile kernel of up to 16 rows has one workgroup per head
+// and takes the same time for 2 rows as for 16; at 12 rows (7B shapes)
+// split took 96 against 114 us at context 4096 (MHA), 70 against 108 (8 kv
+// heads), and 17-20 against 19-20 at 512, but 16 rows favour the tile
+// kernel at short contexts (20 against 25 us). Beyond, the tile kernel (16 query rows per wave on fp32 MFMA, each key and
 // value row loaded once per 16 rows) for head sizes it is built for; other
 // head sizes run the split kernel with one chunk per row (the whole context,
 // in rounds of 64 positions, no merge).
