@@ -119,9 +119,11 @@ typedef struct {
 } em_attention_shape;
 
 /* Replaces enum class AttentionKernel, cuda_attention.h:15-19. */
-#define EM_ATTN_AUTOMATIC 0    /* split for up to 12 rows; more rows: 16-row fp32 MFMA tiles
-                                  (head_size a multiple of 16, at most 128), else one chunk
-                                  per row, no merge */
+#define EM_ATTN_AUTOMATIC 0    /* split for up to 5 rows (12 when seq_len <= 512); more rows:
+                                  16-row fp32 MFMA tiles, also split over the context when
+                                  their grid is small (head_size a multiple of 16, at most
+                                  128), else split for up to 12 rows and then one chunk per
+                                  row, no merge. Scratch for rows serves fewer rows too. */
 #define EM_ATTN_SINGLE_BLOCK 1 /* one workgroup per (head, row), scores in LDS */
 #define EM_ATTN_SPLIT 2        /* positions split across workgroups, merged in chunk order */
 

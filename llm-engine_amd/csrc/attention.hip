@@ -24,13 +24,16 @@
 //    measured slower than a second launch, and the fixed merge order keeps
 //    results bit-identical across calls. A context that fits one chunk is
 //    normalised and written by the first kernel; the merge kernel then exits.
-//    With more than 12 rows (prefill), automatic runs the same kernel with
-//    one chunk per row: the whole context in rounds, no merge.
+//    With more rows (prefill), automatic runs the tile kernel (16
+//    query rows per wave on fp32 MFMA), split over the context as well when
+//    its grid is small; for head sizes it is not built for, the same split
+//    kernel with one chunk per row: the whole context in rounds, no merge.
 //  * single_block (on request): workgroup (head, row) holds the query and
 //    the scores of the whole context in LDS; any head size.
 //
 // The grid is sized for seq_len, never for the position: chunks past the end
 // of a row's context return at once.
+#include <algorithm>
 #include <cmath>
 #include <string>
 
@@ -42,7 +45,7 @@ namespace {
 
 constexpr int kMinChunk = kSplitMinChunk;  // positions per split workgroup, at least
 constexpr int kMaxSplits = 256;         // chunks per (row, head group), at most
-constexpr std::size_t kSplitMaxRows = 12;  // automatic: split up to this many rows
+constexpr std::size_t kSplitMaxRows = 12;  // automatic: split up to this many rows, at most
 constexpr std::size_t kMaxLds = 64 * 1024;  // dynamic LDS per workgroup
 
 int split_count(int seq_len) {
@@ -100,16 +103,21 @@ SplitScratch split_scratch(const AttnShape& s, std::size_t rows) {
     return l;
 }
 
-// automatic: the split kernel with chunks across workgroups for up to 12
-// rows. Its cost grows with the rows (each reads its chunks' keys and
-// values), while a tile kernel of up to 16 rows has one workgroup per head
-// and takes the same time for 2 rows as for 16; at 12 rows (7B shapes)
-// split took 96 against 114 us at context 4096 (MHA), 70 against 108 (8 kv
-// heads), and 17-20 against 19-20 at 512, but 16 rows favour the tile
-// kernel at short contexts (20 against 25 us). Beyond, the tile kernel (16 query rows per wave on fp32 MFMA, each key and
-// value row loaded once per 16 rows) for head sizes it is built for; other
-// head sizes run the split kernel with one chunk per row (the whole context,
-// in rounds of 64 positions, no merge).
+// automatic: the split kernel with chunks across workgroups for few rows,
+// beyond that the tile kernel (16 query rows per wave on fp32 MFMA, each key
+// and value row loaded once per 16 rows, split over the context when its
+// grid is small) for head sizes it is built for; other head sizes run the
+// split kernel with one chunk per row (the whole context, in rounds of 64
+// positions, no merge) from 13 rows. The split kernel's cost grows with the
+// rows (each reads its chunks' keys and values); the split tile kernel's
+// hardly does below 16. Measured at 7B shapes (MHA / 8 kv heads), split
+// against split tile, us:
+//   context  256, 2-12 rows: 10.0-14.5 / 15.4-15.7, 12.0-14.8 / 14.2-15.4
+//   context 1024, 4 rows:    18.2 / 18.5, 14.9 / 17.4; 8 rows: 25.1 / 19.0, 20.9 / 17.9
+//   context 4096, 4 rows:    48.4 / 41.0, 31.6 / 33.7; 8 rows: 75.4 / 41.1, 51.8 / 33.9
+// The context is read on the device, so the cut goes by seq_len: up to 5
+// rows split when seq_len exceeds 512, up to 12 otherwise (and for head
+// sizes the tile kernel does not take).
 constexpr int kAttnWhole = 3;
 constexpr int kAttnTile = 4;
 constexpr int kTileRows = 16;        // query rows per tile wave
@@ -119,15 +127,56 @@ bool tile_supports(const AttnShape& s) {
     return s.head_size % 16 == 0 && s.head_size <= kTileMaxHeadSize;
 }
 
+// A tile grid of a few row tiles has one workgroup per (head, 16 rows): 32
+// workgroups for 16 rows of a 32-head model, which took 108-114 us at
+// context 4096 whatever the row count. Such a grid is split over the
+// context as well, into chunks of at least kTileChunkMin positions, enough
+// to bring it near kTileTargetGroups workgroups; each chunk leaves its
+// unnormalised softmax for the merge kernel, as the split kernel's do.
+// Grids of 512 workgroups or more are not split.
+constexpr int kTileChunkMin = 256;
+constexpr long long kTileTargetGroups = 1024;
+
+int tile_splits(const AttnShape& s, std::size_t rows) {
+    const long long tiles = static_cast<long long>(s.n_heads) *
+                            static_cast<long long>((rows + kTileRows - 1) / kTileRows);
+    if (tiles >= kTileTargetGroups / 2) return 1;
+    const long long want = (kTileTargetGroups + tiles - 1) / tiles;
+    const long long cap = (s.seq_len + kTileChunkMin - 1) / kTileChunkMin;
+    return static_cast<int>(std::max(1LL, std::min(want, cap)));
+}
+
+// Positions per chunk: a multiple of 64, so chunks are whole 16-position
+// blocks, and splits chunks cover seq_len.
+int tile_chunk(const AttnShape& s, int splits) {
+    const int c = (s.seq_len + splits - 1) / splits;
+    return (c + 63) / 64 * 64;
+}
+
+SplitScratch tile_scratch(const AttnShape& s, std::size_t rows, int splits) {
+    const std::size_t blocks = rows * s.n_heads * static_cast<std::size_t>(splits);
+    auto up4 = [](std::size_t x) { return (x + 3) / 4 * 4; };
+    SplitScratch l{};
+    l.o = 0;
+    l.ml = up4(blocks * s.head_size);
+    l.total = l.ml + up4(2 * blocks);
+    return l;
+}
+
+std::size_t split_max_rows(const AttnShape& s) {
+    return tile_supports(s) && s.seq_len > 512 ? 5 : kSplitMaxRows;
+}
+
 int resolve(int kernel, std::size_t rows, const AttnShape& s) {
     if (kernel != kAttnAutomatic) return kernel;
-    if (rows <= kSplitMaxRows) return kAttnSplit;
+    if (rows <= split_max_rows(s)) return kAttnSplit;
     return tile_supports(s) ? kAttnTile : kAttnWhole;
 }
 
 struct AttnArgs {
     int n_heads, head_size, group, seq_len, splits, chunk_cap, rows;
     int merge_from;  // the merge kernel takes rows of at least this many chunks (>= 2)
+    int tile_chunk;  // tile kernel split over the context: positions per chunk (0: no split)
     int q_stride, kv_stride, out_stride;
     const int* pos;
     const float* q;
@@ -417,7 +466,7 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
     const int h = blockIdx.x / groups, d0 = (blockIdx.x % groups) * dpw;
     const int i = blockIdx.y;
     const int n_ctx = *a.pos + i + 1;
-    const int chunk = chunk_size(n_ctx, a.splits);
+    const int chunk = a.tile_chunk ? a.tile_chunk : chunk_size(n_ctx, a.splits);
     const int n = (n_ctx + chunk - 1) / chunk;
     if (n < a.merge_from) return;  // one chunk: written by the split kernel; few: by their consumer
     const std::size_t b = (static_cast<std::size_t>(i) * a.n_heads + h) * a.splits;
@@ -606,6 +655,12 @@ __global__ __launch_bounds__(kTileWaves * kWave) void attn_tile_kernel(AttnArgs 
     const int row = min(r0 + j, a.rows - 1);  // rows past the call: computed, not stored
     const int pq = pos0 + row;                // this lane's query position
     const int last = pos0 + min(r0 + kTileRows - 1, a.rows - 1);  // the wave's last position
+    // Split over the context: this workgroup takes positions [lo, hi] of
+    // chunk blockIdx.z (none past last: the grid is sized for seq_len).
+    const int cz = blockIdx.z;
+    const int lo = cz * a.tile_chunk;
+    if (lo > last) return;
+    const int hi = a.tile_chunk ? min(last, lo + a.tile_chunk - 1) : last;
     const float* kbase = a.kc + static_cast<std::size_t>((h / a.group) * HS);
     const float* vbase = a.vc + static_cast<std::size_t>((h / a.group) * HS);
 
@@ -670,10 +725,11 @@ __global__ __launch_bounds__(kTileWaves * kWave) void attn_tile_kernel(AttnArgs 
         m = mn;
     };
 
-    // This wave's blocks: [nb * w / 4, nb * (w + 1) / 4) of the tile's nb.
-    const int nb = last / KB + 1;
-    const int first = KB * (nb * wave / kTileWaves);
-    const int wlast = KB * (nb * (wave + 1) / kTileWaves) - 1;  // < first: no blocks
+    // This wave's blocks: [nb * w / 4, nb * (w + 1) / 4) of the nb blocks
+    // from lo (a multiple of 16) through hi.
+    const int b0i = lo / KB, nb = hi / KB + 1 - b0i;
+    const int first = KB * (b0i + nb * wave / kTileWaves);
+    const int wlast = KB * (b0i + nb * (wave + 1) / kTileWaves) - 1;  // < first: no blocks
     if (first <= wlast) {
         TileBlock<E> b0, b1;
         load(b0, first);
@@ -693,9 +749,11 @@ __global__ __launch_bounds__(kTileWaves * kWave) void attn_tile_kernel(AttnArgs 
     for (int c = 0; c < E; ++c) os[wave][c][lane] = o[c];
     __syncthreads();
     if (wave != 0) return;
+    // M is finite for every query with a position in [lo, hi] (the others
+    // are not stored): some wave holds that position.
     float M = ms[0][lane];
 #pragma unroll
-    for (int w = 1; w < kTileWaves; ++w) M = fmaxf(M, ms[w][lane]);  // finite: wave 0 has position 0
+    for (int w = 1; w < kTileWaves; ++w) M = fmaxf(M, ms[w][lane]);
     l = 0.0f;
 #pragma unroll
     for (int c = 0; c < E; ++c) o[c] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -712,7 +770,22 @@ __global__ __launch_bounds__(kTileWaves * kWave) void attn_tile_kernel(AttnArgs 
     // the xor pairs add them in the same order in every lane.
     l += __shfl_xor(l, 16, kWave);
     l += __shfl_xor(l, 32, kWave);
-    if (r0 + j < a.rows) {
+    // Split: a query whose context spans more than one chunk leaves this
+    // chunk's (max, sum, unnormalised output) for the merge kernel; one whose
+    // context fits chunk 0 is written here, as the split kernel writes it.
+    if (r0 + j < a.rows && a.tile_chunk && pq >= a.tile_chunk && lo <= pq) {
+        const std::size_t b = (static_cast<std::size_t>(r0 + j) * a.n_heads + h) * a.splits + cz;
+        floatx4* dst = reinterpret_cast<floatx4*>(a.part_o + b * HS + Q4 * g);
+        float run[Q4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int c = 0; c < E; ++c) run[E * r + c] = o[c][r];
+#pragma unroll
+        for (int u = 0; u < E; ++u)
+            dst[u] = floatx4{run[4 * u], run[4 * u + 1], run[4 * u + 2], run[4 * u + 3]};
+        if (g == 0) a.part_ml[b] = make_float2(M, l);
+    } else if (r0 + j < a.rows && cz == 0 && (a.tile_chunk == 0 || pq < a.tile_chunk)) {
         const float inv = 1.0f / l;
         floatx4* dst = reinterpret_cast<floatx4*>(a.out + static_cast<std::size_t>(r0 + j) * a.out_stride +
                                                   static_cast<std::size_t>(h) * HS + Q4 * g);
@@ -728,7 +801,7 @@ __global__ __launch_bounds__(kTileWaves * kWave) void attn_tile_kernel(AttnArgs 
 }
 
 void launch_tile(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t stream) {
-    const dim3 grid(s.n_heads, (rows + kTileRows - 1) / kTileRows);
+    const dim3 grid(s.n_heads, (rows + kTileRows - 1) / kTileRows, a.tile_chunk ? a.splits : 1);
     const dim3 block(kTileWaves * kWave);
     switch (s.head_size / 16) {
         case 1: hipLaunchKernelGGL(attn_tile_kernel<1>, grid, block, 0, stream, a); break;
@@ -797,10 +870,25 @@ std::string attention_reject(const AttnShape& s, int kernel) {
     return "";
 }
 
+// Enough for any call of up to `rows` rows, so that a buffer sized once for
+// the most rows serves every smaller call: a split tile grid's chunk count
+// grows as its row tiles shrink.
 std::size_t attention_scratch_floats(const AttnShape& s, std::size_t rows, int kernel) {
     if (kernel == kAttnSingle) return 0;
-    if (kernel == kAttnAutomatic) rows = rows < kSplitMaxRows ? rows : kSplitMaxRows;
-    return split_scratch(s, rows).total;
+    if (kernel != kAttnAutomatic) return split_scratch(s, rows).total;
+    const std::size_t cut = split_max_rows(s);
+    std::size_t need = split_scratch(s, rows < cut ? rows : cut).total;
+    if (rows > cut && tile_supports(s)) {
+        const std::size_t tiles = (rows + kTileRows - 1) / kTileRows;
+        for (std::size_t rt = 1; rt <= tiles; ++rt) {
+            const std::size_t m = std::min(rows, rt * kTileRows);
+            if (m <= cut) continue;
+            const int S = tile_splits(s, m);
+            if (S == 1) break;  // more row tiles split no further
+            need = std::max(need, tile_scratch(s, m, S).total);
+        }
+    }
+    return need;
 }
 
 bool attention_uses_split(const AttnShape& s, std::size_t rows, int kernel) {
@@ -848,7 +936,20 @@ void run_attention(const AttnShape& s, int rows, const int* pos, const float* q,
     kernel = resolve(kernel, rows, s);
     AttnArgs a = base_args(s, rows, pos, q, kc, vc, out);
     if (kernel == kAttnTile) {
+        // The context split needs the caller's scratch (sized by
+        // attention_scratch_floats); without it the grid stays whole.
+        const int S = scratch && reinterpret_cast<uintptr_t>(scratch) % 16 == 0
+                          ? tile_splits(s, static_cast<std::size_t>(rows))
+                          : 1;
+        if (S > 1) {
+            const SplitScratch l = tile_scratch(s, static_cast<std::size_t>(rows), S);
+            a.splits = S;
+            a.tile_chunk = tile_chunk(s, S);
+            a.part_o = scratch + l.o;
+            a.part_ml = reinterpret_cast<float2*>(scratch + l.ml);
+        }
         launch_tile(s, a, rows, stream);
+        if (S > 1) launch_merge(s, a, rows, stream);
         return;
     }
     if (kernel == kAttnSingle) {

@@ -70,10 +70,13 @@ def test_kernels_match_double_reference(case, kernel):
 
 # Prefill rows (automatic, more than 12): the tile kernel for head sizes that
 # are multiples of 16 up to 128 (every register layout it is built for, MHA,
-# GQA, MQA), the one-chunk-per-row split kernel for the rest (20, 144).
+# GQA, MQA), the one-chunk-per-row split kernel for the rest (20, 144). These
+# grids have few heads, so the tile kernel also splits the context into
+# chunks of 256 positions or more and merges them (at 3000 positions, up to
+# 12 chunks); rows whose context fits the first chunk are written directly.
 PREFILL_CASES = [(4, 4, 16, 200), (8, 2, 64, 700), (4, 1, 80, 300), (2, 1, 96, 300),
                  (3, 3, 112, 200), (8, 2, 128, 700), (6, 6, 48, 256), (4, 4, 32, 300),
-                 (4, 2, 20, 200), (2, 2, 144, 300)]
+                 (4, 2, 20, 200), (2, 2, 144, 300), (4, 2, 128, 3000)]
 
 
 @pytest.mark.parametrize("case", PREFILL_CASES, ids=lambda c: "x".join(map(str, c)))
