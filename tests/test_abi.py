@@ -116,6 +116,30 @@ def test_attention_check_rejects_like_the_reference():
     assert em.attention_scratch_floats(S(4, 4, 8, 64, 64, 32, 32), 3, "split") > 0
 
 
+def test_attention_scratch_for_rows_serves_fewer_rows():
+    # automatic may split the tile kernel over the context too, and a grid of
+    # fewer row tiles takes more chunks, so the size for `rows` must cover
+    # every smaller call: it never shrinks as rows grow, and it holds the
+    # split tile's (max, sum, output) for each row, head and chunk, with
+    # chunks = min(ceil(1024 / (heads * ceil(rows / 16))), ceil(seq_len / 256))
+    # wherever that grid has under 512 workgroups and more than one chunk.
+    em = engine.load()
+    for heads, kv, hs, T in ((32, 8, 128, 4096), (32, 32, 128, 1024), (8, 2, 64, 700),
+                             (4, 2, 128, 3000), (6, 6, 48, 256)):
+        shape = em.attention_shape(heads, kv, hs, T)
+        cut = 5 if T > 512 else 12
+        prev = 0
+        for rows in range(1, min(T, 600) + 1):
+            n = em.attention_scratch_floats(shape, rows, "automatic")
+            assert n >= prev, (heads, hs, T, rows)
+            prev = n
+            tiles = heads * -(-rows // 16)
+            if rows > cut and tiles < 512:
+                chunks = min(-(-1024 // tiles), -(-T // 256))
+                if chunks > 1:
+                    assert n >= rows * heads * chunks * (hs + 2), (heads, hs, T, rows)
+
+
 def test_stream_read_checks_before_the_gpu():
     # Size and alignment are rejected on the host, GPU or not; zero bytes is
     # a no-op.
