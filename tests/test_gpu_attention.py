@@ -82,12 +82,13 @@ PREFILL_CASES = [(4, 4, 16, 200), (8, 2, 64, 700), (4, 1, 80, 300), (2, 1, 96, 3
 @pytest.mark.parametrize("case", PREFILL_CASES, ids=lambda c: "x".join(map(str, c)))
 def test_prefill_rows_match_double_reference(case):
     # Row counts that fill 16-row tiles exactly and leave them ragged;
-    # starting positions on and across 16-position block edges, and the end
-    # of the cache.
+    # starting positions on and across 16-position block edges, rows on both
+    # sides of a split tile's first chunk edge (position 256) in one tile,
+    # and the end of the cache.
     T = case[3]
     worst = 0.0
     for i, rows in enumerate((13, 16, 17, 40, 100)):
-        worst = max(worst, run_case(case, "automatic", (0, 15, 16, 31, 33, T - rows),
+        worst = max(worst, run_case(case, "automatic", (0, 15, 16, 31, 33, 250, T - rows),
                                     rows, seed=7400 + 10 * i))
     print(f"{case} prefill: worst {worst:.2e}")
 
