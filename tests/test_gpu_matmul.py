@@ -326,6 +326,47 @@ SPLIT_SHAPES = [(9, 300, 32), (12, 4096, 4096), (24, 4096, 4096), (64, 4096, 409
                 (512, 4096, 12288), (300, 520, 12288), (200, 301, 32768), (2048, 1024, 4096)]
 
 
+# automatic's cuts below 9 rows, on both sides: int8 B goes to the exact-split
+# kernel from 5 rows, from 3 at 2^25 weights and from 2 at 2^26; fp32 B to
+# tiled_split from 4 rows at 2^25. (m, k, n, int8)
+ROUTING_CASES = [(2, 4096, 8176, True), (2, 4096, 8192, True), (3, 4096, 8192, True),
+                 (4, 4096, 4096, True), (5, 4096, 4096, True), (8, 2048, 4112, True),
+                 (2, 4096, 16384, True), (3, 4096, 8176, True),
+                 (3, 4096, 8192, False), (4, 4096, 8192, False), (8, 4096, 8192, False),
+                 (4, 4096, 8176, False)]
+
+
+@pytest.mark.parametrize("case", ROUTING_CASES, ids=lambda c: "x".join(map(str, c[:3])) +
+                         ("_q8" if c[3] else "_f32"))
+def test_automatic_small_m_routing_matches_oracle(case):
+    # Whichever kernel automatic picks at these sizes, with and without the
+    # fused norm and accumulation, every element within the north star's
+    # 1e-4 * sum_k |a||w|.
+    m, k, n, q8 = case
+    A = inputs.normal((m, k), 1.0, 521 + m)
+    C0 = inputs.normal((m, n), 1.0, 522)
+    w = inputs.uniform((k,), 0.5, 1.5, 523)
+    if q8:
+        q, s = orc.quantize_q8(inputs.normal((k, n), 0.02, 524))
+        Bf = orc.dequantize(q, s)
+        B, scale = dev(q), dev(s)
+    else:
+        Bf = inputs.normal((k, n), 0.02, 524)
+        B, scale = dev(Bf), None
+    An = orc.rmsnorm(A, w)
+    for norm in (False, True):
+        Ause = An if norm else A
+        want = orc.matmul_f64(Ause, Bf) + C0.astype(np.float64)
+        bound = orc.abs_bound(Ause, Bf)
+        C = dev(C0)
+        em.matmul(dev(A), B, C, scale=scale, accumulate=True,
+                  rms_weight=dev(w) if norm else None)
+        got = host(C).astype(np.float64)
+        ratio = float((np.abs(got - want) / np.maximum(bound, 1e-30)).max())
+        print(f"{case} norm={norm}: max |err| / sum|a||w| = {ratio:.2e}")
+        assert ratio <= 1e-4, (case, norm, ratio)
+
+
 @pytest.mark.parametrize("shape", SPLIT_SHAPES, ids=lambda s: "x".join(map(str, s)))
 def test_exact_split_tighter_than_fp32_tolerance(shape):
     # automatic sends int8 B above 8 rows to the exact-split bf16 kernel: with A
