@@ -103,7 +103,20 @@ void run_naive(const MatmulArgs& a);
 // (split_bf16.hip). Fuses the norm. Needs n % 16 == 0 and 16-byte aligned B
 // and scales.
 bool split_bf16_supports(const MatmulArgs& a);
-void run_split_bf16(const MatmulArgs& a);
+// The forward pass's RoPE and cache write for a qkv product (columns: q at
+// 0, k at dim, v at dim + kv_dim), rows at positions *pos + i.
+struct RopeFuse {
+    const int* pos;
+    const float* cos_t;
+    const float* sin_t;
+    float* kc;
+    float* vc;
+    int dim, kv_dim, head_size;
+};
+// With rope, and when the product needs no k split (it writes C directly):
+// q is stored rotated, k rotated into kc and v into vc (not into C), with
+// rope_cache_kernel's arithmetic; returns true. Otherwise C as usual, false.
+bool run_split_bf16(const MatmulArgs& a, const RopeFuse* rope = nullptr);
 // True if automatic sends an int8 product of m rows (k x n weights) to the
 // exact-split kernel rather than the GEMV. EM_SPLIT_MIN_ROWS (2 or more)
 // replaces the rule by a row threshold, for sweeps.

@@ -216,6 +216,7 @@ private:
                           const float* ssq);
     bool residual(int n, const float* in, const Proj& w);
     bool residual_merged(const SplitRow& att, const Proj& w);
+    bool qkv_exact_split(int n, LayerDev& L, bool* roped);
     bool swiglu_w2(const Summed& gu, const Proj& w2, bool* wrote_ssq);
     void reserve_rows(std::size_t n);
     void enqueue(int n);
@@ -396,6 +397,23 @@ bool Model::residual(int n, const float* in, const Proj& w) {
     return slices > 1;
 }
 
+// Prefill rows whose int8 qkv product goes to the exact-split kernel (as
+// project() would send it): with RoPE and the cache write in the product's
+// epilogue when it needs no k split (*roped; k and v then reach only the
+// caches), else qkv_ as project() leaves it. The same bits either way as
+// project() followed by rope_cache_kernel. False: not this path.
+bool Model::qkv_exact_split(int n, LayerDev& L, bool* roped) {
+    const MatmulArgs a = gemv_args(n, x_.p, L.wqkv, qkv_.p, L.rms_att.p, false, nullptr);
+    if (!q8_ || n < 2 || !split_bf16_preferred(a.m, a.n, a.k) || !split_bf16_supports(a))
+        return false;
+    const RopeFuse r{feed_dev_.p, rope_cos_.p, rope_sin_.p, L.kcache.p, L.vcache.p,
+                     static_cast<int>(cfg_.dim), static_cast<int>(shape_.kv_stride),
+                     shape_.head_size};
+    *roped = run_split_bf16(a, &r);
+    check(hipGetLastError(), "launch");
+    return true;
+}
+
 // x += att W for one decode row whose attention chunks are not merged yet:
 // the GEMV merges them in its A staging (run_skinny_merged), one launch
 // fewer; for a shape it does not take, the merge kernel writes att first.
@@ -456,8 +474,12 @@ void Model::enqueue(int n) {
     const int rope_threads = D / 2 + KV / 2 + KV;
     const int swiglu_blocks = std::min(ceil_div(static_cast<long long>(n) * H, kThreads), 4096);
     for (LayerDev& L : layers_) {
-        const Summed qkv = project_summed(n, x_.p, L.wqkv, qkv_.p, L.rms_att.p,
-                                          have_ssq ? ssq_.p : nullptr);
+        bool roped = false;
+        Summed qkv{qkv_.p, nullptr, nullptr, 1, qkv_cols,
+                   static_cast<std::size_t>(n) * qkv_cols};
+        if (!(n > 1 && qkv_exact_split(n, L, &roped)))
+            qkv = project_summed(n, x_.p, L.wqkv, qkv_.p, L.rms_att.p,
+                                 have_ssq ? ssq_.p : nullptr);
         // One row: RoPE and the cache write inside the attention launch,
         // and the chunks' merge inside the wo GEMV.
         SplitRow chunks{};
@@ -465,9 +487,11 @@ void Model::enqueue(int n) {
                                            rope_sin_.p, L.kcache.p, L.vcache.p, att_.p,
                                            attn_scratch_.p, stream_,
                                            merge_kernel_ ? nullptr : &chunks))) {
-            hipLaunchKernelGGL(rope_cache_kernel, dim3(ceil_div(rope_threads, kThreads), n),
-                               dim3(kThreads), 0, stream_, qkv, qkv_cols, D, KV, hs, feed_dev_.p,
-                               rope_cos_.p, rope_sin_.p, qkv_.p, L.kcache.p, L.vcache.p);
+            if (!roped)
+                hipLaunchKernelGGL(rope_cache_kernel, dim3(ceil_div(rope_threads, kThreads), n),
+                                   dim3(kThreads), 0, stream_, qkv, qkv_cols, D, KV, hs,
+                                   feed_dev_.p, rope_cos_.p, rope_sin_.p, qkv_.p, L.kcache.p,
+                                   L.vcache.p);
             run_attention(shape_, n, feed_dev_.p, qkv_.p, L.kcache.p, L.vcache.p, att_.p,
                           attn_scratch_.p, kAttnAutomatic, stream_);
         }

@@ -182,7 +182,30 @@ struct SbParams {
     float* out;  // C (direct) or partials [slice][m][n]
     int accumulate, direct;
     int row_tiles, col_tiles, xcd_order;
+    RopeFuse rope;  // direct only: rope.pos non-null fuses RoPE and the cache write
 };
+
+// rope_cache_kernel's work on columns c .. c + 3 of row `row` (c % 4 == 0,
+// head_size % 4 == 0): two q or k pairs rotated by rope_pair with the
+// tables' row of this position, q back into C, k into the key cache; v
+// into the value cache.
+__device__ __forceinline__ void rope_store(const SbParams& p, int row, int c, floatx4 v) {
+    const RopeFuse& r = p.rope;
+    const int pos = *r.pos + row, half = r.head_size / 2;
+    if (c < r.dim + r.kv_dim) {
+        const bool is_k = c >= r.dim;
+        const int cc = is_k ? c - r.dim : c;
+        const int a0 = pos * half + (cc / 2) % half, a1 = pos * half + (cc / 2 + 1) % half;
+        const float2 y0 = rope_pair(v[0], v[1], r.cos_t[a0], r.sin_t[a0]);
+        const float2 y1 = rope_pair(v[2], v[3], r.cos_t[a1], r.sin_t[a1]);
+        float* dst = is_k ? r.kc + static_cast<std::size_t>(pos) * r.kv_dim + cc
+                          : p.out + static_cast<std::size_t>(row) * p.n + c;
+        *reinterpret_cast<floatx4*>(dst) = floatx4{y0.x, y0.y, y1.x, y1.y};
+    } else {
+        *reinterpret_cast<floatx4*>(r.vc + static_cast<std::size_t>(pos) * r.kv_dim +
+                                    (c - r.dim - r.kv_dim)) = v;
+    }
+}
 
 template <int RB, bool RAW>
 struct Chunk {
@@ -394,6 +417,10 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
                         &tile[(ww * 16 + orow) * kTileStride + ocol + 4 * q]);
                 if (p.direct) {
                     v *= *reinterpret_cast<const floatx4*>(p.scale + c);
+                    if (p.rope.pos) {
+                        rope_store(p, row, c, v);
+                        continue;
+                    }
                     floatx4* o = reinterpret_cast<floatx4*>(p.out + static_cast<std::size_t>(row) * p.n + c);
                     *o = p.accumulate ? *o + v : v;
                 } else {
@@ -447,7 +474,7 @@ bool split_bf16_preferred(int m, int n, int k) {
     return m >= 5 || (m >= 3 && w >= (1LL << 25)) || (m >= 2 && w >= (1LL << 26));
 }
 
-void run_split_bf16(const MatmulArgs& a) {
+bool run_split_bf16(const MatmulArgs& a, const RopeFuse* rope) {
     static const int forced_rb = [] {
         const char* v = std::getenv("EM_SPLIT_ROW_BLOCKS");
         const int x = v ? std::atoi(v) : 0;
@@ -537,6 +564,10 @@ void run_split_bf16(const MatmulArgs& a) {
     // XCD-grouped order, which gives each XCD a contiguous run of B (4096 x
     // 32000, m = 5: 26.6 against 28.6 us in plain order).
     p.xcd_order = row_tiles == 1 && col_tiles % 8 == 0 ? 0 : 1;
+    const bool fuse = rope && p.direct && !a.accumulate && rope->head_size % 4 == 0 &&
+                      rope->dim % 4 == 0 && rope->kv_dim % 4 == 0 &&
+                      a.n == rope->dim + 2 * rope->kv_dim;
+    if (fuse) p.rope = *rope;
     const int total = static_cast<int>(blocks) * slices;
     switch (RB) {
         case 1: launch<1>(p, total, raw, a.stream); break;
@@ -544,6 +575,7 @@ void run_split_bf16(const MatmulArgs& a) {
         default: launch<2>(p, total, raw, a.stream); break;
     }
     if (!p.direct) run_reduce_slices(a.m, a.n, slices, p.out, a.scale, a.C, a.accumulate, a.stream);
+    return fuse;
 }
 
 }  // namespace em
