@@ -77,10 +77,13 @@ def gemv_bytes(m: int, k: int, n: int, q8: bool) -> int:
 
 
 class Pool:
-    """POOL copies of a K x N weight matrix (int8 + scales, or fp32) on the GPU."""
+    """POOL copies of a K x N weight matrix (int8 + scales, or fp32) on the GPU;
+    with packed, int8 copies are kept in the strip layout (em_pack_q8) only."""
 
-    def __init__(self, em, torch, q8: bool, k: int, n: int, copies: int, seed: int):
+    def __init__(self, em, torch, q8: bool, k: int, n: int, copies: int, seed: int,
+                 packed: bool = False):
         self.q8 = q8
+        self.packed = packed
         self.ws, self.scales = [], []
         g = torch.Generator(device="cuda")
         for i in range(copies):
@@ -88,6 +91,10 @@ class Pool:
             W = torch.randn((k, n), generator=g, device="cuda", dtype=torch.float32) * 0.02
             if q8:
                 q, s = em.quantize_q8(W)
+                if packed:
+                    pq = em.pack_q8(q)
+                    del q
+                    q = pq
                 self.ws.append(q)
                 self.scales.append(s)
                 del W
@@ -97,19 +104,26 @@ class Pool:
         torch.cuda.synchronize()
 
 
+def pool_product(em, A, C, pool, w, s):
+    if pool.packed:
+        em.matmul_packed(A, w, C.shape[1], s, C)
+    else:
+        em.matmul(A, w, C, scale=s)
+
+
 def capture_step(em, torch, A, C, pool: Pool):
     """A HIP graph of one sweep over the pool."""
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):  # warm the library's scratch outside capture
         for w, s in zip(pool.ws, pool.scales):
-            em.matmul(A, w, C, scale=s)
+            pool_product(em, A, C, pool, w, s)
     torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         for w, s in zip(pool.ws, pool.scales):
-            em.matmul(A, w, C, scale=s)
+            pool_product(em, A, C, pool, w, s)
     torch.cuda.synchronize()
     return graph
 
@@ -130,10 +144,11 @@ def time_graph(torch, graph, steps: int, warmup: int):
     return start.elapsed_time(end) / 1e3, wall
 
 
-def gemv_case(em, torch, m, q8, steps, warmup, copies=None, seed=1000, k=DIM, n=DIM):
+def gemv_case(em, torch, m, q8, steps, warmup, copies=None, seed=1000, k=DIM, n=DIM,
+              packed=False):
     per_copy = k * n * (1 if q8 else 4)
     copies = copies or max(2, -(-POOL_MIN_BYTES // per_copy))
-    pool = Pool(em, torch, q8, k, n, copies, seed)
+    pool = Pool(em, torch, q8, k, n, copies, seed, packed=packed)
     g = torch.Generator(device="cuda")
     g.manual_seed(7 + m)
     A = torch.randn((m, k), generator=g, device="cuda", dtype=torch.float32)
@@ -490,6 +505,150 @@ def hbm_ceiling(em, torch, nbytes: int = POOL_MIN_BYTES, reps: int = 5) -> dict:
     return out
 
 
+def graph_of(torch, fn, count: int):
+    """A HIP graph of `count` back-to-back calls fn(i) on a side stream
+    (one eager pass first, so nothing allocates during capture)."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for i in range(count):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(count):
+            fn(i)
+    torch.cuda.synchronize()
+    return graph
+
+
+FLOOR_BLOCKS = (256, 512, 1024, 2048, 4096)
+FLOOR_DEPTHS = (4, 8, 16)
+
+
+def floor_study(em, torch, reps: int = 20) -> dict:
+    """What bounds one int8 m = 1 4096^2 call, measured with the bench's method
+    (HIP-graph replay of back-to-back dependent launches, HIP events):
+      empty     an empty kernel per launch (1, 256 = the GEMV's grid, 1024 workgroups)
+      read16    em_probe_read of one 16 MiB pool copy per launch over 38 copies
+                (608 MiB, past the Infinity Cache), swept over workgroups,
+                loads in flight per thread and access pattern
+      read600   the same sweep as one launch over a 600 MiB buffer (the ceiling)
+      gemv      the int8 GEMV variants of em_probe_gemv_q8 over the headline's
+                38-copy quantised pool: 0 product path (two launches), 1 and 2
+                one launch with the in-kernel arrival, 4 one launch with k split
+                in two halves that meet through an atomic exchange word per output
+      gemv_packed  em_matmul_q8_packed over the same weights in the strip layout"""
+    out = {"method": "HIP-graph replay, HIP events on torch's stream; us per launch"}
+    copies = 38
+    launches = 2 * copies
+    emp = {}
+    for blocks in (1, 256, 1024):
+        g = graph_of(torch, lambda i, b=blocks: em.probe_empty(b), launches)
+        secs, _ = time_graph(torch, g, reps, 3)
+        emp[str(blocks)] = round(secs / (reps * launches) * 1e6, 3)
+        del g
+    out["empty_us"] = emp
+    progress("floor: empty kernels done")
+
+    mib16 = 16 << 20
+    bufs = [torch.randint(-127, 128, (mib16,), dtype=torch.int8, device="cuda")
+            for _ in range(copies)]
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    r16 = {}
+    for contig in (True, False):
+        for blocks in FLOOR_BLOCKS:
+            for depth in FLOOR_DEPTHS:
+                g = graph_of(torch, lambda i, b=blocks, d=depth, c=contig:
+                             em.probe_read(bufs[i % copies], sink, b, d, c), copies)
+                secs, _ = time_graph(torch, g, reps, 3)
+                us = secs / (reps * copies) * 1e6
+                r16[f"{'contig' if contig else 'stride'} b{blocks} d{depth}"] = \
+                    {"us": round(us, 3), "GBps": round(mib16 / us / 1e3, 1)}
+                del g
+    out["read16"] = r16
+    best = min(r16.items(), key=lambda kv: kv[1]["us"])
+    out["read16_best"] = {"config": best[0], **best[1]}
+    progress("floor: 16 MiB reads done")
+    del bufs
+
+    big = torch.ones((600 << 20) // 4, dtype=torch.float32, device="cuda")
+    r600 = {}
+    for contig in (True, False):
+        for blocks in FLOOR_BLOCKS:
+            for depth in FLOOR_DEPTHS:
+                fn = lambda b=blocks, d=depth, c=contig: em.probe_read(big, sink, b, d, c)
+                fn()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(5):
+                    fn()
+                e1.record()
+                torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / 5
+                r600[f"{'contig' if contig else 'stride'} b{blocks} d{depth}"] = \
+                    {"us": round(us, 1), "GBps": round((600 << 20) / us / 1e3, 1)}
+    out["read600"] = r600
+    best = min(r600.items(), key=lambda kv: kv[1]["us"])
+    out["read600_best"] = {"config": best[0], **best[1]}
+    del big
+    progress("floor: 600 MiB reads done")
+
+    pool = Pool(em, torch, True, DIM, DIM, copies, 1000)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(8)
+    A = torch.randn((1, DIM), generator=g, device="cuda", dtype=torch.float32)
+    counters = torch.zeros(DIM // 256, dtype=torch.int32, device="cuda")
+    ref = torch.empty((1, DIM), device="cuda")
+    em.probe_gemv_q8(A, pool.ws[0], pool.scales[0], ref, 0)
+    gv = {}
+    for variant in (0, 1, 2, 4):
+        C = torch.zeros((1, DIM), device="cuda")
+        g = graph_of(torch, lambda i, v=variant: em.probe_gemv_q8(
+            A, pool.ws[i % copies], pool.scales[i % copies], C, v, counters), copies)
+        secs, _ = time_graph(torch, g, reps, 3)
+        del g
+        us = secs / (reps * copies) * 1e6
+        row = {"us": round(us, 3), "GBps": round(gemv_bytes(1, DIM, DIM, True) / us / 1e3, 1)}
+        C.zero_()
+        em.probe_gemv_q8(A, pool.ws[0], pool.scales[0], C, variant, counters)
+        C2 = torch.zeros_like(C)
+        em.probe_gemv_q8(A, pool.ws[0], pool.scales[0], C2, variant, counters)
+        torch.cuda.synchronize()
+        row["equal_to_product_path"] = bool(torch.equal(C, ref))
+        row["repeat_identical"] = bool(torch.equal(C, C2))
+        # against |A| x |W| (the tolerance's scale): 1e-4 is the bar
+        bound = (A.abs() @ (pool.ws[0].float().abs() * pool.scales[0])).clamp_min(1e-30)
+        row["max_err_over_abs_bound_vs_product"] = float(((C - ref).abs() / bound).max())
+        gv[str(variant)] = row
+    out["gemv"] = gv
+    out["counters_left_zero"] = bool(torch.count_nonzero(counters).item() == 0)
+    packed = [em.pack_q8(w) for w in pool.ws]
+    C = torch.zeros((1, DIM), device="cuda")
+    g = graph_of(torch, lambda i: em.matmul_packed(A, packed[i % copies], DIM,
+                                                   pool.scales[i % copies], C), copies)
+    secs, _ = time_graph(torch, g, reps, 3)
+    del g
+    us = secs / (reps * copies) * 1e6
+    C.zero_()
+    em.matmul_packed(A, packed[0], DIM, pool.scales[0], C)
+    C2 = torch.zeros_like(C)
+    em.matmul_packed(A, packed[0], DIM, pool.scales[0], C2)
+    torch.cuda.synchronize()
+    bound = (A.abs() @ (pool.ws[0].float().abs() * pool.scales[0])).clamp_min(1e-30)
+    out["gemv_packed"] = {"us": round(us, 3),
+                          "GBps": round(gemv_bytes(1, DIM, DIM, True) / us / 1e3, 1),
+                          "repeat_identical": bool(torch.equal(C, C2)),
+                          "max_err_over_abs_bound_vs_product": float(((C - ref).abs() / bound).max())}
+    del packed
+    del pool
+    torch.cuda.synchronize()
+    progress("floor: GEMV variants done")
+    return out
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -556,6 +715,9 @@ def main() -> int:
                     help="only time the Llama-7B-shaped forward pass L layers deep (32 for "
                          "the full model; builds ~0.8 GB of host weights per layer) and print "
                          "its JSON line")
+    ap.add_argument("--floor", action="store_true",
+                    help="only the floor study of the headline call (empty launches, "
+                         "16 MiB and 600 MiB read sweeps, single-launch GEMV variants)")
     ap.add_argument("--profile-pass", nargs="?", const="gemv", choices=["gemv", "gemm", "split", "prefill", "decode"],
                     help="eager launches for rocprofv3 --pmc: gemv (calibration copy + "
                          "headline, the default), gemm (fp32 tiled N=4096), split "
@@ -585,6 +747,9 @@ def main() -> int:
             print(json.dumps({"done": "mha" if kv == 32 else "gqa8", **r}), file=sys.stderr,
                   flush=True)
         print(json.dumps(out))
+        return 0
+    if args.floor:
+        print(json.dumps(floor_study(em, torch)))
         return 0
     if args.profile_pass == "gemm":
         print(json.dumps(profile_gemm_pass(em, torch)))

@@ -88,6 +88,27 @@ int em_matmul_q8(size_t m, size_t n, size_t k, const float* A, const int8_t* B,
                  const float* scale, float* C, int kernel, int accumulate,
                  const float* rms_weight, void* stream);
 
+/* ---- Strip layout of int8 weights (explicit opt-in) ------------------------
+ * The reference keeps int8 weights row-major (QTensor, tensor.h:23-28); the
+ * entry points above take that layout. The strip layout is an opt-in copy for
+ * decode-shaped products: n / 16 strips of 16 columns, strip j holding rows
+ * 0 .. k - 1 of columns 16j .. 16j + 15 contiguously,
+ *     packed[(j * k + r) * 16 + t] = B[r * n + 16 j + t],
+ * the same bytes reordered (scales unchanged). An m <= 8 product over it is
+ * one launch with no split-K partials. Needs n % 16 == 0 and 16-byte aligned
+ * buffers of k * n bytes. No counterpart in the reference. */
+int em_pack_q8(size_t k, size_t n, const int8_t* B, int8_t* packed, void* stream);
+int em_unpack_q8(size_t k, size_t n, const int8_t* packed, int8_t* B, void* stream);
+/* C = A x dequantize(B) (C += if accumulate; A replaced by rmsnorm(A) *
+ * rms_weight when given), B in the strip layout: the semantics of
+ * em_matmul_q8 for m <= 8 rows, in one launch, bit-identical across repeats.
+ * EM_EINVAL for m > 8, n % 16 != 0, a misaligned B, more than 2^31
+ * elements; m == 0 or n == 0 does nothing; k == 0 zeroes C unless
+ * accumulating. */
+int em_matmul_q8_packed(size_t m, size_t n, size_t k, const float* A, const int8_t* packed,
+                        const float* scale, float* C, int accumulate, const float* rms_weight,
+                        void* stream);
+
 /* Symmetric per-column int8 quantisation on the GPU, bit-exact with
  *   QTensor quantize_q8(const Tensor& B)   quant.h:7, quant.cpp:6-28
  * B is rows x cols fp32 on the device; q receives rows x cols int8 and scale
@@ -107,6 +128,25 @@ int em_dequantize_q8(size_t rows, size_t cols, const int8_t* q, const float* sca
  * (bench_cuda.cpp:79-88); it is for callers that measure the matmul path.
  * `sink` is 4 bytes of device memory the kernel may write (almost never). */
 int em_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream);
+
+/* Measurement entry points for bench.py's floor study (no counterpart in the
+ * reference; not part of the matmul interface). em_probe_empty launches an
+ * empty kernel of `blocks` 256-thread workgroups. em_probe_read reads `bytes`
+ * at `buf` once with `blocks` workgroups and `depth` (4, 8 or 16) 16-byte
+ * loads in flight per thread, each workgroup on one contiguous chunk
+ * (contiguous != 0) or the grid striding over the buffer. em_probe_gemv_q8
+ * runs one variant of the int8 one-row GEMV (m == 1, n % 16 == 0, 16-byte
+ * aligned B): 0 the product path (GEMV, then the slice sum, as em_matmul_q8),
+ * 1 one launch whose last workgroup per 256-column tile adds the slices
+ * (counters: ceil(n / 256) ints of device memory, zero, left zero), 2 the same
+ * with the partials stored as agent-scope atomic stores, 4 one launch with k
+ * split in two halves that meet through an atomic exchange word per output
+ * (k <= 8192). Every variant writes C. */
+int em_probe_empty(unsigned blocks, void* stream);
+int em_probe_read(const void* buf, size_t bytes, uint32_t* sink, unsigned blocks, unsigned depth,
+                  int contiguous, void* stream);
+int em_probe_gemv_q8(size_t m, size_t n, size_t k, const float* A, const int8_t* B,
+                     const float* scale, float* C, int variant, int* counters, void* stream);
 
 /* ---- Causal attention over a KV cache (cuda_attention.h) ------------------ */
 

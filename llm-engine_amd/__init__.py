@@ -29,6 +29,8 @@ EXPORTS = (
     "em_last_error", "em_available", "em_synchronize", "em_scratch_generation",
     "em_malloc", "em_free", "em_memcpy_h2d", "em_memcpy_d2h",
     "em_matmul_f32", "em_matmul_q8", "em_quantize_q8", "em_dequantize_q8", "em_stream_read",
+    "em_probe_empty", "em_probe_read", "em_probe_gemv_q8",
+    "em_pack_q8", "em_unpack_q8", "em_matmul_q8_packed",
     "em_attention_check", "em_attention_scratch_floats", "em_attention",
     "em_model_create", "em_model_destroy", "em_model_forward",
 )
@@ -117,6 +119,13 @@ def lib() -> ctypes.CDLL:
         L.em_quantize_q8.argtypes = [_sz, _sz, _vp, _vp, _vp, _vp]
         L.em_dequantize_q8.argtypes = [_sz, _sz, _vp, _vp, _vp, _vp]
         L.em_stream_read.argtypes = [_vp, _sz, _vp, _vp]
+        L.em_pack_q8.argtypes = [_sz, _sz, _vp, _vp, _vp]
+        L.em_unpack_q8.argtypes = [_sz, _sz, _vp, _vp, _vp]
+        L.em_matmul_q8_packed.argtypes = [_sz, _sz, _sz, _vp, _vp, _vp, _vp, ctypes.c_int, _vp,
+                                          _vp]
+        L.em_probe_empty.argtypes = [ctypes.c_uint, _vp]
+        L.em_probe_read.argtypes = [_vp, _sz, _vp, ctypes.c_uint, ctypes.c_uint, ctypes.c_int, _vp]
+        L.em_probe_gemv_q8.argtypes = [_sz, _sz, _sz, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _vp]
         shp = ctypes.POINTER(AttentionShape)
         L.em_attention_check.argtypes = [shp, ctypes.c_int]
         L.em_attention_scratch_floats.argtypes = [shp, _sz, ctypes.c_int]
@@ -235,6 +244,60 @@ def stream_read(buf, sink, stream=None) -> None:
     on torch's current stream; sink is a 1-element int32 device tensor."""
     _check(lib().em_stream_read(buf.data_ptr(), buf.numel() * buf.element_size(),
                                 sink.data_ptr(), _stream_ptr(stream)))
+
+
+def pack_q8(q, stream=None):
+    """The strip layout (em_pack_q8) of a row-major int8 device matrix [k, n]:
+    a new int8 tensor of the same size, 1-D."""
+    import torch
+    k, n = q.shape
+    packed = torch.empty((k * n,), dtype=torch.int8, device=q.device)
+    _check(lib().em_pack_q8(k, n, _dev(q, torch.int8), packed.data_ptr(), _stream_ptr(stream)))
+    return packed
+
+
+def unpack_q8(packed, k: int, n: int, stream=None):
+    """Row-major [k, n] int8 from the strip layout (em_unpack_q8)."""
+    import torch
+    q = torch.empty((k, n), dtype=torch.int8, device=packed.device)
+    _check(lib().em_unpack_q8(k, n, _dev(packed, torch.int8), q.data_ptr(), _stream_ptr(stream)))
+    return q
+
+
+def matmul_packed(A, packed, n: int, scale, C=None, *, accumulate=False, rms_weight=None,
+                  stream=None):
+    """C = [C +] rmsnorm?(A) x B with B in the strip layout (em_matmul_q8_packed)."""
+    import torch
+    m, k = A.shape
+    if C is None:
+        C = torch.empty((m, n), dtype=torch.float32, device=A.device)
+    rw = _dev(rms_weight, torch.float32) if rms_weight is not None else None
+    _check(lib().em_matmul_q8_packed(m, n, k, _dev(A, torch.float32), _dev(packed, torch.int8),
+                                     _dev(scale, torch.float32), _dev(C, torch.float32),
+                                     int(bool(accumulate)), rw, _stream_ptr(stream)))
+    return C
+
+
+def probe_empty(blocks: int, stream=None) -> None:
+    """em_probe_empty: one empty launch of `blocks` workgroups."""
+    _check(lib().em_probe_empty(blocks, _stream_ptr(stream)))
+
+
+def probe_read(buf, sink, blocks: int, depth: int, contiguous: bool, stream=None) -> None:
+    """em_probe_read over a device tensor's bytes."""
+    _check(lib().em_probe_read(buf.data_ptr(), buf.numel() * buf.element_size(), sink.data_ptr(),
+                               blocks, depth, int(bool(contiguous)), _stream_ptr(stream)))
+
+
+def probe_gemv_q8(A, q, scale, C, variant: int, counters=None, stream=None) -> None:
+    """em_probe_gemv_q8: one variant of the int8 one-row GEMV (see the header)."""
+    import torch
+    m, k = A.shape
+    n = q.shape[1]
+    cnt = _dev(counters, torch.int32) if counters is not None else None
+    _check(lib().em_probe_gemv_q8(m, n, k, _dev(A, torch.float32), _dev(q, torch.int8),
+                                  _dev(scale, torch.float32), _dev(C, torch.float32), variant,
+                                  cnt, _stream_ptr(stream)))
 
 
 def dequantize_q8(q, scale, stream=None):

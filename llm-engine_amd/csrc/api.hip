@@ -18,6 +18,12 @@
 #include "llm_engine_amd.h"
 
 namespace em {
+
+std::string shapes(std::size_t m, std::size_t n, std::size_t k) {
+    return "(A is " + std::to_string(m) + "x" + std::to_string(k) + ", B is " + std::to_string(k) +
+           "x" + std::to_string(n) + ")";
+}
+
 namespace {
 
 thread_local std::string g_error;
@@ -35,10 +41,6 @@ bool too_many(std::size_t a, std::size_t b) {
     return a != 0 && b > kLimit / a;
 }
 
-std::string shapes(std::size_t m, std::size_t n, std::size_t k) {
-    return "(A is " + std::to_string(m) + "x" + std::to_string(k) + ", B is " + std::to_string(k) +
-           "x" + std::to_string(n) + ")";
-}
 
 template <class BT>
 int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, const BT* B,
@@ -158,6 +160,26 @@ float* scratch(ScratchSlot slot, std::size_t floats) {
 }
 
 std::size_t scratch_generation() { return g_generation.load(); }
+
+unsigned long long* exchange_words(std::size_t count) {
+    static unsigned long long* words = nullptr;
+    static std::size_t cap = 0;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (count > cap) {
+        hip_check(hipDeviceSynchronize(), "synchronize before exchange-word growth");
+        if (words) hip_check(hipFree(words), "free exchange words");
+        words = nullptr;
+        cap = 0;
+        void* p = nullptr;
+        hip_check(hipMalloc(&p, count * sizeof(unsigned long long)), "alloc exchange words");
+        hip_check(hipMemset(p, 0, count * sizeof(unsigned long long)), "clear exchange words");
+        hip_check(hipDeviceSynchronize(), "clear exchange words");
+        words = static_cast<unsigned long long*>(p);
+        cap = count;
+        g_generation.fetch_add(1);
+    }
+    return words;
+}
 
 
 int cu_count() {
@@ -283,6 +305,85 @@ int em_dequantize_q8(size_t rows, size_t cols, const int8_t* q, const float* sca
 }
 
 
+int em_pack_q8(size_t k, size_t n, const int8_t* B, int8_t* packed, void* stream) {
+    if (too_many(k, n)) return fail(EM_EINVAL, "pack_q8: more than 2^31 elements");
+    if (n % 16) return fail(EM_EINVAL, "pack_q8: n must be a multiple of 16 (B is " +
+                                           std::to_string(k) + "x" + std::to_string(n) + ")");
+    if (k == 0 || n == 0) return EM_OK;
+    if (!B || !packed) return fail(EM_EINVAL, "pack_q8: null pointer");
+    if (reinterpret_cast<uintptr_t>(B) % 16 || reinterpret_cast<uintptr_t>(packed) % 16)
+        return fail(EM_EINVAL, "pack_q8: B and packed must be 16-byte aligned");
+    if (!em::device_present()) return fail(EM_ENODEV, "pack_q8: no usable GPU");
+    try {
+        em::run_pack_strips(static_cast<int>(k), static_cast<int>(n), B, packed,
+                            static_cast<hipStream_t>(stream));
+        em::hip_check(hipGetLastError(), "launch");
+    } catch (const std::exception& e) {
+        return fail(EM_EDEVICE, e.what());
+    }
+    return EM_OK;
+}
+
+int em_unpack_q8(size_t k, size_t n, const int8_t* packed, int8_t* B, void* stream) {
+    if (too_many(k, n)) return fail(EM_EINVAL, "unpack_q8: more than 2^31 elements");
+    if (n % 16) return fail(EM_EINVAL, "unpack_q8: n must be a multiple of 16");
+    if (k == 0 || n == 0) return EM_OK;
+    if (!B || !packed) return fail(EM_EINVAL, "unpack_q8: null pointer");
+    if (reinterpret_cast<uintptr_t>(B) % 16 || reinterpret_cast<uintptr_t>(packed) % 16)
+        return fail(EM_EINVAL, "unpack_q8: B and packed must be 16-byte aligned");
+    if (!em::device_present()) return fail(EM_ENODEV, "unpack_q8: no usable GPU");
+    try {
+        em::run_unpack_strips(static_cast<int>(k), static_cast<int>(n), packed, B,
+                              static_cast<hipStream_t>(stream));
+        em::hip_check(hipGetLastError(), "launch");
+    } catch (const std::exception& e) {
+        return fail(EM_EDEVICE, e.what());
+    }
+    return EM_OK;
+}
+
+int em_matmul_q8_packed(size_t m, size_t n, size_t k, const float* A, const int8_t* packed,
+                        const float* scale, float* C, int accumulate, const float* rms_weight,
+                        void* stream) {
+    if (m > 8)
+        return fail(EM_EINVAL, "matmul_q8_packed: the strip layout takes at most 8 rows " +
+                                   em::shapes(m, n, k));
+    if (too_many(m, k) || too_many(k, n) || too_many(m, n))
+        return fail(EM_EINVAL, "matmul_q8_packed: more than 2^31 elements " + em::shapes(m, n, k));
+    if (n % 16)
+        return fail(EM_EINVAL, "matmul_q8_packed: n must be a multiple of 16 " + em::shapes(m, n, k));
+    if (m == 0 || n == 0) return EM_OK;
+    if (!C) return fail(EM_EINVAL, "matmul_q8_packed: C is null " + em::shapes(m, n, k));
+    if (k && (!A || !packed || !scale))
+        return fail(EM_EINVAL, "matmul_q8_packed: A, B or scale is null " + em::shapes(m, n, k));
+    if (k && reinterpret_cast<uintptr_t>(packed) % 16)
+        return fail(EM_EINVAL, "matmul_q8_packed: packed B must be 16-byte aligned");
+    if (!em::device_present()) return fail(EM_ENODEV, "matmul_q8_packed: no usable GPU");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    try {
+        if (k == 0) {
+            if (!accumulate) em::run_fill_zero(C, m * n, s);
+        } else {
+            em::MatmulArgs a{};
+            a.m = static_cast<int>(m);
+            a.n = static_cast<int>(n);
+            a.k = static_cast<int>(k);
+            a.A = A;
+            a.B = packed;
+            a.scale = scale;
+            a.C = C;
+            a.accumulate = accumulate != 0;
+            a.rms_weight = rms_weight;
+            a.stream = s;
+            em::run_gemv_packed(a, packed);
+        }
+        em::hip_check(hipGetLastError(), "launch");
+    } catch (const std::exception& e) {
+        return fail(EM_EDEVICE, e.what());
+    }
+    return EM_OK;
+}
+
 int em_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream) {
     if (bytes == 0) return EM_OK;
     if (!buf || !sink) return fail(EM_EINVAL, "stream_read: null pointer");
@@ -291,6 +392,59 @@ int em_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream) 
     if (!em::device_present()) return fail(EM_ENODEV, "stream_read: no usable GPU");
     try {
         em::run_stream_read(buf, bytes, sink, static_cast<hipStream_t>(stream));
+        em::hip_check(hipGetLastError(), "launch");
+    } catch (const std::exception& e) {
+        return fail(EM_EDEVICE, e.what());
+    }
+    return EM_OK;
+}
+
+int em_probe_empty(unsigned blocks, void* stream) {
+    if (blocks == 0 || blocks > 65535) return fail(EM_EINVAL, "probe_empty: 1..65535 workgroups");
+    if (!em::device_present()) return fail(EM_ENODEV, "probe_empty: no usable GPU");
+    em::run_probe_empty(static_cast<int>(blocks), static_cast<hipStream_t>(stream));
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail(EM_EDEVICE, std::string("hip: launch: ") + hipGetErrorString(err));
+    return EM_OK;
+}
+
+int em_probe_read(const void* buf, size_t bytes, uint32_t* sink, unsigned blocks, unsigned depth,
+                  int contiguous, void* stream) {
+    if (bytes == 0) return EM_OK;
+    if (!buf || !sink) return fail(EM_EINVAL, "probe_read: null pointer");
+    if (bytes % 16 || reinterpret_cast<uintptr_t>(buf) % 16)
+        return fail(EM_EINVAL, "probe_read: buffer and size must be multiples of 16 bytes");
+    if (blocks == 0 || blocks > 65535) return fail(EM_EINVAL, "probe_read: 1..65535 workgroups");
+    if (depth != 4 && depth != 8 && depth != 16)
+        return fail(EM_EINVAL, "probe_read: depth must be 4, 8 or 16");
+    if (!em::device_present()) return fail(EM_ENODEV, "probe_read: no usable GPU");
+    em::run_probe_read(buf, bytes, static_cast<int>(blocks), static_cast<int>(depth),
+                       contiguous != 0, sink, static_cast<hipStream_t>(stream));
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail(EM_EDEVICE, std::string("hip: launch: ") + hipGetErrorString(err));
+    return EM_OK;
+}
+
+int em_probe_gemv_q8(size_t m, size_t n, size_t k, const float* A, const int8_t* B,
+                     const float* scale, float* C, int variant, int* counters, void* stream) {
+    if (m != 1 || n == 0 || k == 0 || too_many(k, n) || n % 16)
+        return fail(EM_EINVAL, "probe_gemv_q8: one row, n a multiple of 16, k > 0");
+    if (!A || !B || !scale || !C || (variant != 0 && !counters))
+        return fail(EM_EINVAL, "probe_gemv_q8: null pointer");
+    if (!em::device_present()) return fail(EM_ENODEV, "probe_gemv_q8: no usable GPU");
+    em::MatmulArgs a{};
+    a.m = 1;
+    a.n = static_cast<int>(n);
+    a.k = static_cast<int>(k);
+    a.A = A;
+    a.B = B;
+    a.scale = scale;
+    a.C = C;
+    a.stream = static_cast<hipStream_t>(stream);
+    try {
+        if (!em::run_skinny_probe(a, variant, counters))
+            return fail(EM_EINVAL, "probe_gemv_q8: variant " + std::to_string(variant) +
+                                       " does not take this shape");
         em::hip_check(hipGetLastError(), "launch");
     } catch (const std::exception& e) {
         return fail(EM_EDEVICE, e.what());

@@ -1,0 +1,428 @@
+// Decode-shaped products (m <= 8) over int8 weights held in the strip layout,
+// one launch per product: an explicit opt-in weight format behind the
+// boundary (the reference keeps QTensor row-major, tensor.h:23-28, and its
+// decode product is sgemm_skinny + sum_slices, cuda_matmul.cu:189-254,
+// 365-397).
+//
+// Strip layout. A k x n int8 matrix (n % 16 == 0) is stored as n / 16 strips
+// of 16 columns; strip j holds rows 0 .. k - 1 of columns 16j .. 16j + 15,
+// 16 bytes a row, contiguously:
+//     packed[(j * k + r) * 16 + t] = B[r * n + 16 j + t].
+// The bytes are the quantised bytes, only reordered, and the column scales
+// are unchanged.
+//
+// Why. In row-major order a contiguous run of a row holds many columns, so
+// spreading one m = 1 product over the chip means splitting k across
+// workgroups, writing partials and adding them in a second launch. On gfx950
+// a dependent launch costs ~1.6 us, about 70 % of the 2.4 us the 16 MiB of a
+// 4096^2 int8 matrix take to stream once a launch is running. In the strip
+// layout one workgroup reads all of k for its 16 columns as one contiguous
+// run, so no partial leaves the workgroup and the product is one launch.
+//
+//  * Workgroup = one strip (256 threads). Lane t takes rows t, t + 256, ...:
+//    each load instruction of a wave reads 1 KiB of consecutive rows. All
+//    loads of a batch (L rows per lane) are in flight before any is used;
+//    with more than one batch the next batch loads while this one is summed.
+//  * int8 is widened in registers and summed unscaled; the column scale is
+//    applied once to the reduced sum.
+//  * The 64 lanes of a wave are reduced by a fixed reduce-scatter (16 values
+//    per lane -> one column per lane: lane swaps across halves and rows, DPP
+//    inside rows), the four waves in LDS in wave order. Every order is fixed,
+//    so repeated calls give the same bits.
+//  * A is staged in LDS per batch (float4 loads issued before the weights,
+//    so waiting for them does not wait for the weight stream).
+//  * With a norm weight, the workgroup forms the row's RMS scale from a pass
+//    over A (fixed order) while its first weights are in flight, and
+//    normalises each A value as it uses it, as rmsnorm_rows does.
+#include <algorithm>
+#include <cstdlib>
+
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace em {
+namespace {
+
+constexpr int kStrip = 16;  // columns per strip
+
+struct PackedParams {
+    int m, n, k;
+    const float* A;
+    const float* rms_weight;
+    const int8_t* P;  // strip layout
+    const float* scale;
+    float* C;
+    int accumulate;
+};
+
+// Thread t of a 256-thread workgroup copies 16 bytes: strip j, row r with
+// j * k + r = global index, so the writes are contiguous.
+__global__ __launch_bounds__(kThreads) void pack_strips_kernel(int k, int n, const int8_t* B,
+                                                               int8_t* P) {
+    const long long strips = n / kStrip;
+    const long long total = strips * k;
+    for (long long i = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x; i < total;
+         i += static_cast<long long>(gridDim.x) * kThreads) {
+        const long long j = i / k, r = i - j * k;
+        const uint4 v = *reinterpret_cast<const uint4*>(B + r * n + j * kStrip);
+        *reinterpret_cast<uint4*>(P + i * kStrip) = v;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void unpack_strips_kernel(int k, int n, const int8_t* P,
+                                                                 int8_t* B) {
+    const long long strips = n / kStrip;
+    const long long total = strips * k;
+    for (long long i = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x; i < total;
+         i += static_cast<long long>(gridDim.x) * kThreads) {
+        const long long j = i / k, r = i - j * k;
+        *reinterpret_cast<uint4*>(B + r * n + j * kStrip) =
+            *reinterpret_cast<const uint4*>(P + i * kStrip);
+    }
+}
+
+// Sum over the 64 lanes, per column: on entry lane l holds 16 column sums
+// v[0..15]; on exit lane l holds the wave's total of column l >> 2 (the four
+// lanes of a group hold the same bits). Four halving steps, each adding a
+// lane's kept half to its partner's copy of the same half, then two full
+// steps:
+//   distance 32: v_permlane32_swap exchanges x's upper 32 lanes with y's
+//                lower 32, so x + y gives lanes 0-31 column i and lanes
+//                32-63 column i + 8 (x = v[i], y = v[i + 8]);
+//   distance 16: v_permlane16_swap exchanges x's odd rows of 16 with y's
+//                even rows, the same way;
+//   distance 8, 4: DPP row_shl / row_shr inside a row of 16, the lane's bit
+//                picking which half it keeps;
+//   distance 2, 1: DPP quad permutations (both lanes compute a + b in some
+//                order; the sum is the same bits either way).
+// Every value is added exactly once in a fixed place, so the result does not
+// depend on timing. No LDS is touched.
+__device__ __forceinline__ float dpp_f(float v, int ctrl) {
+    switch (ctrl) {  // the control must be a constant of the instruction
+        case 0x108: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x108, 0xf, 0xf, false));
+        case 0x118: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x118, 0xf, 0xf, false));
+        case 0x104: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x104, 0xf, 0xf, false));
+        case 0x114: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x114, 0xf, 0xf, false));
+        case 0xB1: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));
+        default: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));
+    }
+}
+
+__device__ __forceinline__ float wave_reduce_scatter16(float (&v)[16]) {
+    const int lane = threadIdx.x % kWave;
+    float a8[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]),
+                                                        __float_as_uint(v[i + 8]), false, false);
+        a8[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    float a4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a8[i]),
+                                                        __float_as_uint(a8[i + 4]), false, false);
+        a4[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    // DPP reads a lane that is switched off as zero, so both sides of each
+    // choice are formed by every lane (outside any branch), then selected.
+    const bool b3 = lane & 8, b2 = lane & 4;
+    float a2[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {  // row_shl:8 reads lane + 8, row_shr:8 lane - 8
+        const float keep_lo = a4[i] + dpp_f(a4[i], 0x108);
+        const float keep_hi = a4[i + 2] + dpp_f(a4[i + 2], 0x118);
+        a2[i] = b3 ? keep_hi : keep_lo;
+    }
+    const float keep_lo = a2[0] + dpp_f(a2[0], 0x104);
+    const float keep_hi = a2[1] + dpp_f(a2[1], 0x114);
+    float a1 = b2 ? keep_hi : keep_lo;
+    a1 += dpp_f(a1, 0xB1);  // quad_perm [1, 0, 3, 2]: lane ^ 1
+    a1 += dpp_f(a1, 0x4E);  // quad_perm [2, 3, 0, 1]: lane ^ 2
+    return a1;
+}
+
+// Sum over the workgroup's NW waves, every thread gets the result: wave
+// sums by a fixed butterfly, then added in wave order. `part` holds NW
+// floats of LDS; the leading barrier lets a previous use finish.
+template <int NW>
+__device__ __forceinline__ float group_sum(float v, float* part) {
+    v = wave_sum(v);
+    __syncthreads();
+    if (threadIdx.x % kWave == 0) part[threadIdx.x / kWave] = v;
+    __syncthreads();
+    float t = part[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) t += part[w];
+    return t;
+}
+
+// NT threads per workgroup (one strip), L rows per lane per batch.
+// VEC: k % 4 == 0 and A 16-byte aligned (A staged as float4). MULTI: k is
+// more than one batch (the next batch loads while this one is summed).
+template <int NT, int MM, int L, bool NORM, bool VEC, bool MULTI>
+__global__ __launch_bounds__(NT) void gemv_packed_kernel(PackedParams p) {
+    constexpr int NW = NT / kWave;
+    constexpr int RB = NT * L;              // rows of the strip per batch
+    constexpr int NF = MM * RB / 4 / NT;    // A float4s per thread per batch
+    static_assert(NF >= 1 && MM * RB % (4 * NT) == 0, "whole float4 slots per thread");
+    __shared__ float4 a_s4[MM * RB / 4];
+    __shared__ float red[NW][MM][kStrip];
+    __shared__ float part[NW];
+    const float* a_s = reinterpret_cast<const float*>(a_s4);
+    const int tid = threadIdx.x;
+    const int strip = blockIdx.x;
+    const int8_t* base = p.P + static_cast<size_t>(strip) * p.k * kStrip;
+    const int batches = MULTI ? (p.k + RB - 1) / RB : 1;
+
+    // This thread's output in the epilogue (row er, column ec).
+    const int er = tid / kStrip, ej = tid % kStrip;
+    const int ec = strip * kStrip + ej;
+    const bool eout = tid < MM * kStrip && er < p.m;
+
+    // A of batch b, raw: slot s = tid + NT t holds row r = s / (RB / 4) of
+    // A, values b * RB + 4 (s % (RB / 4)) .. + 3. Loads are unconditional
+    // (indices clamped into A); what lies past k or m is zeroed when the
+    // slot is written to LDS.
+    auto load_a = [&](int b, float4 (&av)[NF]) {
+#pragma unroll
+        for (int t = 0; t < NF; ++t) {
+            const int sl = tid + t * NT;
+            const int r = min(sl / (RB / 4), p.m - 1);
+            const int j = b * RB + 4 * (sl % (RB / 4));
+            const float* row = p.A + static_cast<size_t>(r) * p.k;
+            if constexpr (VEC) {
+                av[t] = *reinterpret_cast<const float4*>(row + min(j, p.k - 4));
+            } else {
+                av[t] = make_float4(row[min(j, p.k - 1)], row[min(j + 1, p.k - 1)],
+                                    row[min(j + 2, p.k - 1)], row[min(j + 3, p.k - 1)]);
+            }
+        }
+    };
+    auto store_a = [&](int b, const float4 (&av)[NF]) {
+#pragma unroll
+        for (int t = 0; t < NF; ++t) {
+            const int sl = tid + t * NT;
+            const int r = sl / (RB / 4);
+            const int j = b * RB + 4 * (sl % (RB / 4));
+            const bool rin = r < p.m;
+            float4 v = av[t];
+            v.x = rin && j < p.k ? v.x : 0.0f;
+            v.y = rin && j + 1 < p.k ? v.y : 0.0f;
+            v.z = rin && j + 2 < p.k ? v.z : 0.0f;
+            v.w = rin && j + 3 < p.k ? v.w : 0.0f;
+            a_s4[sl] = v;
+        }
+    };
+    // Weights of batch b: rows b * RB + tid + NT i (past k: row k - 1, whose
+    // A value is zero).
+    auto load_w = [&](int b, uint4 (&w)[L]) {
+#pragma unroll
+        for (int i = 0; i < L; ++i) {
+            const int row = min(b * RB + tid + i * NT, p.k - 1);
+            w[i] = stream_load(reinterpret_cast<const uint4*>(base + static_cast<size_t>(row) * kStrip));
+        }
+    };
+
+    float acc[MM][kStrip];
+#pragma unroll
+    for (int r = 0; r < MM; ++r)
+#pragma unroll
+        for (int j = 0; j < kStrip; ++j) acc[r][j] = 0.0f;
+    auto fma_batch = [&](const uint4 (&w)[L], const float (&rs)[MM], int b) {
+#pragma unroll
+        for (int i = 0; i < L; ++i) {
+            float bv[kStrip];
+            widen4(w[i].x, bv);
+            widen4(w[i].y, bv + 4);
+            widen4(w[i].z, bv + 8);
+            widen4(w[i].w, bv + 12);
+            const int pl = tid + i * NT;
+#pragma unroll
+            for (int r = 0; r < MM; ++r) {
+                float a = a_s[r * RB + pl];
+                if constexpr (NORM) {
+                    const int row = b * RB + pl;
+                    a = row < p.k ? a * rs[r] * p.rms_weight[row] : 0.0f;
+                }
+#pragma unroll
+                for (int j = 0; j < kStrip; ++j) acc[r][j] = fmaf(a, bv[j], acc[r][j]);
+            }
+        }
+    };
+
+    // With a norm, the row's RMS scale comes first: a pass over A summing
+    // squares in a fixed order (per thread, then the workgroup), as
+    // rmsnorm_rows. It runs while the first weights are in flight.
+    float rs[MM];
+    float4 av[NF];
+    uint4 w[L];
+    load_a(0, av);
+    load_w(0, w);
+    __builtin_amdgcn_sched_barrier(0);
+    // The epilogue's scale (and prior C) behind the weights: in flight with
+    // them, and waited for only at the end. (Issued before the weights, the
+    // scales, cold like the weights, held up the A staging's wait, which
+    // counts loads in issue order: 5.9 against 5.5 us at 4096^2.)
+    const float esc = p.scale[ec];
+    const float eprior = p.accumulate ? p.C[static_cast<size_t>(min(er, p.m - 1)) * p.n + ec] : 0.0f;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < MM; ++r) rs[r] = 1.0f;
+    if constexpr (NORM) {
+#pragma unroll
+        for (int r = 0; r < MM; ++r) {
+            float ss = 0.0f;
+            if (r < p.m)
+                for (int j = tid; j < p.k; j += NT) {
+                    const float v = p.A[static_cast<size_t>(r) * p.k + j];
+                    ss = fmaf(v, v, ss);
+                }
+            rs[r] = 1.0f / sqrtf(group_sum<NW>(ss, part) / static_cast<float>(p.k) + kRmsEps);
+        }
+    }
+    store_a(0, av);
+    __syncthreads();
+    if constexpr (!MULTI) {
+        fma_batch(w, rs, 0);
+    } else {
+        for (int b = 0; b < batches; ++b) {
+            uint4 wn[L];
+            const bool more = b + 1 < batches;
+            if (more) {
+                load_a(b + 1, av);
+                load_w(b + 1, wn);
+            }
+            fma_batch(w, rs, b);
+            __syncthreads();
+            if (more) {
+                store_a(b + 1, av);
+#pragma unroll
+                for (int i = 0; i < L; ++i) w[i] = wn[i];
+            }
+            __syncthreads();
+        }
+    }
+
+    const int wave = tid / kWave, lane = tid % kWave;
+#pragma unroll
+    for (int r = 0; r < MM; ++r) {
+        const float s = wave_reduce_scatter16(acc[r]);
+        if ((lane & 3) == 0) red[wave][r][lane >> 2] = s;
+    }
+    __syncthreads();
+    if (eout) {
+        float total = red[0][er][ej];
+#pragma unroll
+        for (int w2 = 1; w2 < NW; ++w2) total += red[w2][er][ej];
+        total *= esc;
+        p.C[static_cast<size_t>(er) * p.n + ec] = p.accumulate ? eprior + total : total;
+    }
+}
+
+// Threads per workgroup: 256 by default; EM_PACKED_THREADS (256, 512 or
+// 1024) overrides it for tuning sweeps.
+int packed_threads() {
+    static const int nt = [] {
+        const char* v = std::getenv("EM_PACKED_THREADS");
+        const int x = v ? std::atoi(v) : 0;
+        return x == 512 || x == 1024 ? x : 256;
+    }();
+    return nt;
+}
+
+// Rows per lane L for MM rows of A: capped at LMAX (more rows of A hold
+// more accumulators and A values per lane). One batch holds NT x L rows.
+template <int NT, int MM, bool NORM, bool VEC, int LMAX>
+void launch_depth(int L, const PackedParams& p, hipStream_t s) {
+    const dim3 grid(p.n / kStrip);
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(NT), 0, s, p); };
+    if (L > LMAX) L = LMAX;
+    if (NT * L < p.k) {
+        // Several batches, half as deep, so the next batch's loads fit
+        // beside this one's.
+        constexpr int LM = LMAX >= 8 ? LMAX / 2 : LMAX;
+        return go(gemv_packed_kernel<NT, MM, LM, NORM, VEC, true>);
+    }
+    if (L <= 4) return go(gemv_packed_kernel<NT, MM, 4, NORM, VEC, false>);
+    if constexpr (LMAX >= 8) {
+        if (L <= 8) return go(gemv_packed_kernel<NT, MM, 8, NORM, VEC, false>);
+    }
+    if constexpr (LMAX >= 16) {
+        if (L <= 16) return go(gemv_packed_kernel<NT, MM, 16, NORM, VEC, false>);
+    }
+    if constexpr (LMAX >= 32) go(gemv_packed_kernel<NT, MM, 32, NORM, VEC, false>);
+}
+
+// The shallowest L (4 .. LMAX) whose batch holds all of k.
+int packed_depth(int nt, int k, int lmax) {
+    int L = 4;
+    while (L < lmax && nt * L < k) L *= 2;
+    return L;
+}
+
+// Rows of A -> rows per lane cap at 256 threads (32, 16, 8, 4 for 1, 2, 4,
+// 8 rows: accumulators and A values per lane grow with the rows). One row
+// may also run 512 or 1024 threads per strip, with 8192 / NT rows per lane
+// at most (the same rows per batch, the register budget per lane shrinking
+// with the waves per SIMD).
+template <bool NORM, bool VEC>
+void launch_threads(const PackedParams& p, hipStream_t s) {
+    if (p.m <= 1) {
+        switch (packed_threads()) {
+            case 1024:
+                return launch_depth<1024, 1, NORM, VEC, 8>(packed_depth(1024, p.k, 8), p, s);
+            case 512:
+                return launch_depth<512, 1, NORM, VEC, 16>(packed_depth(512, p.k, 16), p, s);
+            default:
+                return launch_depth<256, 1, NORM, VEC, 32>(packed_depth(256, p.k, 32), p, s);
+        }
+    }
+    if (p.m <= 2) return launch_depth<256, 2, NORM, VEC, 16>(packed_depth(256, p.k, 16), p, s);
+    if (p.m <= 4) return launch_depth<256, 4, NORM, VEC, 8>(packed_depth(256, p.k, 8), p, s);
+    launch_depth<256, 8, NORM, VEC, 4>(4, p, s);
+}
+
+}  // namespace
+
+void run_pack_strips(int k, int n, const int8_t* B, int8_t* P, hipStream_t stream) {
+    const long long total = static_cast<long long>(n / kStrip) * k;
+    const int blocks = static_cast<int>(std::min<long long>((total + kThreads - 1) / kThreads,
+                                                            static_cast<long long>(cu_count()) * 16));
+    hipLaunchKernelGGL(pack_strips_kernel, dim3(blocks > 0 ? blocks : 1), dim3(kThreads), 0, stream,
+                       k, n, B, P);
+}
+
+void run_unpack_strips(int k, int n, const int8_t* P, int8_t* B, hipStream_t stream) {
+    const long long total = static_cast<long long>(n / kStrip) * k;
+    const int blocks = static_cast<int>(std::min<long long>((total + kThreads - 1) / kThreads,
+                                                            static_cast<long long>(cu_count()) * 16));
+    hipLaunchKernelGGL(unpack_strips_kernel, dim3(blocks > 0 ? blocks : 1), dim3(kThreads), 0,
+                       stream, k, n, P, B);
+}
+
+// One batch when k fits NT x L rows, at the shallowest depth that holds
+// it (L capped by the rows of A: 32, 16, 8, 4 for 1, 2, 4, 8 rows); deeper
+// k loops over batches with the next batch in flight.
+void run_gemv_packed(const MatmulArgs& a, const int8_t* packed) {
+    PackedParams p{};
+    p.m = a.m;
+    p.n = a.n;
+    p.k = a.k;
+    p.A = a.A;
+    p.rms_weight = a.rms_weight;
+    p.P = packed;
+    p.scale = a.scale;
+    p.C = a.C;
+    p.accumulate = a.accumulate ? 1 : 0;
+    const bool vec = a.k % 4 == 0 && reinterpret_cast<uintptr_t>(a.A) % 16 == 0;
+    if (a.rms_weight) {
+        if (vec) launch_threads<true, true>(p, a.stream);
+        else launch_threads<true, false>(p, a.stream);
+    } else {
+        if (vec) launch_threads<false, true>(p, a.stream);
+        else launch_threads<false, false>(p, a.stream);
+    }
+}
+
+}  // namespace em

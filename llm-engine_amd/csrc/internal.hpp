@@ -34,6 +34,10 @@ enum ScratchSlot { kPartial = 0, kNorm = 1, kQuant = 2, kSplitA = 3, kPartialFro
                    kSlots = 5 };
 float* scratch(ScratchSlot slot, std::size_t floats);
 std::size_t scratch_generation();
+// Library-owned exchange words for the one-launch pair GEMV: `count` 64-bit
+// words, zero. Grow-only like scratch() (growth bumps scratch_generation());
+// zeroed when allocated, and every call leaves the words it used zero.
+unsigned long long* exchange_words(std::size_t count);
 
 // Compute units of the current device (cached).
 int cu_count();
@@ -140,6 +144,31 @@ void run_reduce_slices(int m, int n, int slices, const float* partial, const flo
 void run_fill_zero(float* p, std::size_t count, hipStream_t stream);
 // Reads bytes (a multiple of 16) of buf once, 16-byte aligned.
 void run_stream_read(const void* buf, std::size_t bytes, uint32_t* sink, hipStream_t stream);
+
+// Measurement kernels (probes.hip, gemv.hip): an empty launch of `blocks`
+// workgroups; one read of `bytes` (a multiple of 16) by `blocks` workgroups
+// with `depth` (4, 8, 16) loads in flight per thread, contiguous chunks per
+// workgroup or a grid stride (false for another depth); and the int8
+// one-row GEMV variants of run_skinny_probe (false for a shape it does not take).
+void run_probe_empty(int blocks, hipStream_t stream);
+bool run_probe_read(const void* buf, std::size_t bytes, int blocks, int depth, bool contig,
+                    uint32_t* sink, hipStream_t stream);
+bool run_skinny_probe(const MatmulArgs& a, int variant, int* counters);
+
+// One int8 row in one launch (gemv_pair.hip): k split in two halves that
+// meet through an atomic exchange word per output; C (+)= as run_skinny
+// writes it, with the same bits as its two-slice sum. Takes m == 1, no
+// norm, n % 16 == 0, 16-byte aligned B and 2 <= k <= 8192.
+bool gemv_pair_supports(const MatmulArgs& a);
+void run_gemv_pair(const MatmulArgs& a);
+
+// The strip layout of int8 weights (gemv_packed.hip): n / 16 strips of 16
+// columns, strip j holding rows 0 .. k - 1 of columns 16j .. 16j + 15
+// contiguously. n % 16 == 0, both buffers 16-byte aligned.
+void run_pack_strips(int k, int n, const int8_t* B, int8_t* P, hipStream_t stream);
+void run_unpack_strips(int k, int n, const int8_t* P, int8_t* B, hipStream_t stream);
+// C (+)= rmsnorm?(A) x B for m <= 8 rows, B in the strip layout, one launch.
+void run_gemv_packed(const MatmulArgs& a, const int8_t* packed);
 
 void run_quantize_q8(int rows, int cols, const float* B, int8_t* q, float* scale,
                      hipStream_t stream);

@@ -150,3 +150,38 @@ def test_stream_read_checks_before_the_gpu():
     assert L.em_stream_read(16, 24, 16, None) == em.EM_EINVAL
     assert b"multiples of 16" in L.em_last_error()
     assert L.em_stream_read(8, 32, 16, None) == em.EM_EINVAL
+
+
+def test_packed_layout_checks_before_the_gpu():
+    # The strip layout's entry points reject bad shapes and alignment on the
+    # host; m == 0 / n == 0 / k == 0 packing are no-ops.
+    L = em.lib()
+    assert L.em_pack_q8(4, 17, 16, 16, None) == em.EM_EINVAL
+    assert b"multiple of 16" in L.em_last_error()
+    assert L.em_pack_q8(0, 16, None, None, None) == em.EM_OK
+    assert L.em_pack_q8(4, 16, None, 16, None) == em.EM_EINVAL
+    assert L.em_pack_q8(4, 16, 8, 16, None) == em.EM_EINVAL
+    assert b"16-byte aligned" in L.em_last_error()
+    assert L.em_unpack_q8(4, 20, 16, 16, None) == em.EM_EINVAL
+    e = err(lambda: em._check(L.em_matmul_q8_packed(9, 16, 4, 16, 16, 16, 16, 0, None, None)))
+    assert e.code == em.EM_EINVAL and "at most 8 rows" in str(e) and "9x4" in str(e)
+    e = err(lambda: em._check(L.em_matmul_q8_packed(1, 20, 4, 16, 16, 16, 16, 0, None, None)))
+    assert e.code == em.EM_EINVAL and "multiple of 16" in str(e)
+    e = err(lambda: em._check(L.em_matmul_q8_packed(1, 16, 4, 16, 8, 16, 16, 0, None, None)))
+    assert e.code == em.EM_EINVAL and "aligned" in str(e)
+    e = err(lambda: em._check(L.em_matmul_q8_packed(1, 16, 4, 16, 16, None, 16, 0, None, None)))
+    assert e.code == em.EM_EINVAL and "null" in str(e)
+    assert L.em_matmul_q8_packed(0, 16, 4, None, None, None, None, 0, None, None) == em.EM_OK
+    e = err(lambda: em._check(L.em_matmul_q8_packed(1, 1 << 16, 1 << 16, 16, 16, 16, 16, 0,
+                                                    None, None)))
+    assert "2^31" in str(e)
+
+
+def test_probes_check_before_the_gpu():
+    L = em.lib()
+    assert L.em_probe_empty(0, None) == em.EM_EINVAL
+    assert L.em_probe_read(16, 64, 16, 256, 5, 0, None) == em.EM_EINVAL
+    assert b"depth" in L.em_last_error()
+    assert L.em_probe_read(16, 64, 16, 0, 8, 0, None) == em.EM_EINVAL
+    assert L.em_probe_gemv_q8(2, 16, 16, 16, 16, 16, 16, 0, None, None) == em.EM_EINVAL
+    assert L.em_probe_gemv_q8(1, 16, 16, 16, 16, 16, 16, 1, None, None) == em.EM_EINVAL

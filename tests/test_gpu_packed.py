@@ -1,0 +1,131 @@
+"""GPU parity of the strip layout of int8 weights (em_pack_q8 /
+em_matmul_q8_packed) against the CPU oracle.
+
+The layout is an explicit opt-in copy behind the boundary (the reference keeps
+QTensor row-major, tensor.h:23-28), so its products are held to the same
+contract as em_matmul_q8's skinny path: the reference tests' 1e-5 * k (2k
+with fusion, test_cuda.cpp:38-47,126-165) and the north star's
+1e-4 * sum_k |a||w| per element, accumulate and rms fusions, k == 0, and
+bit-identical repeats (test_cuda.cpp:272).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from tests import engine, inputs
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+em = engine.load()
+orc = oracle.oracle()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def strips(q):
+    """The layout by its definition: packed[(j * k + r) * 16 + t] = B[r, 16 j + t]."""
+    k, n = q.shape
+    return np.ascontiguousarray(q.reshape(k, n // 16, 16).transpose(1, 0, 2)).reshape(-1)
+
+
+@pytest.mark.parametrize("shape", [(1, 16), (3, 32), (288, 864), (17, 4096), (4096, 4096),
+                                   (11008, 64)], ids=lambda s: "x".join(map(str, s)))
+def test_pack_layout_and_round_trip(shape):
+    k, n = shape
+    q, _ = orc.quantize_q8(inputs.uniform((k, n), -1.0, 1.0, 5))
+    packed = em.pack_q8(dev(q))
+    got = host(packed)
+    assert np.array_equal(got, strips(q))
+    assert np.array_equal(host(em.unpack_q8(packed, k, n)), q)
+
+
+# (m, k, n): decode rows 1..8 against the stories15M and Llama-7B-shaped
+# projections, a k that needs several 4096-row batches (11008, 8193), and
+# k below one batch or not a multiple of 256.
+SHAPES = [(1, 288, 864), (1, 288, 32000), (1, 768, 288), (1, 4096, 4096), (1, 11008, 4096),
+          (1, 8193, 64), (1, 1, 16), (1, 17, 48), (2, 300, 1536), (3, 4096, 272),
+          (4, 4097, 32), (5, 513, 2048), (8, 1000, 4096), (8, 11008, 64), (6, 20, 16),
+          (7, 2, 160)]
+
+
+def check(got, want, A, Bf, k, factor=1.0, C0=None):
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    assert err.max() <= 1e-5 * max(k, 1) * factor, f"max err {err.max()} (k={k})"
+    bound = orc.abs_bound(A, Bf)
+    if C0 is not None:
+        bound = bound + np.abs(C0)
+    assert np.all(err <= 1e-4 * bound + 1e-30), "1e-4 * sum|a||w| bound exceeded"
+
+
+@pytest.mark.parametrize("fusion", ["plain", "acc", "rms", "rms_acc"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_packed_against_oracle(shape, fusion):
+    m, k, n = shape
+    A = inputs.uniform((m, k), -1.0, 1.0, 21)
+    q, s = orc.quantize_q8(inputs.normal((k, n), 0.02, 22))
+    acc = "acc" in fusion
+    rms = "rms" in fusion
+    C0 = inputs.uniform((m, n), -1.0, 1.0, 23) if acc else None
+    w = inputs.uniform((k,), 0.5, 1.5, 24) if rms else None
+    want = orc.matmul_fused(A, Bq=q, scale=s, w=w, C0=C0)
+    C = dev(C0) if acc else torch.empty((m, n), device="cuda")
+    em.matmul_packed(dev(A), em.pack_q8(dev(q)), n, dev(s), C, accumulate=acc,
+                     rms_weight=dev(w) if rms else None)
+    An = orc.rmsnorm(A, w) if rms else A
+    check(host(C), want, An, orc.dequantize(q, s), k, 2.0 if (acc or rms) else 1.0, C0)
+
+
+def test_packed_matches_rowmajor_path_and_repeats():
+    # Same weights through em_matmul_q8 (row-major, split-K) and the strip
+    # layout: within the tolerance of each other, each bit-identical on repeat.
+    m, k, n = 1, 4096, 4096
+    A = dev(inputs.normal((m, k), 1.0, 31))
+    q, s = em.quantize_q8(dev(inputs.normal((k, n), 0.02, 32)))
+    packed = em.pack_q8(q)
+    outs = []
+    for _ in range(3):
+        outs.append(host(em.matmul_packed(A, packed, n, s)))
+    assert all(np.array_equal(outs[0], o) for o in outs[1:])
+    row = host(em.matmul(A, q, scale=s))
+    bound = orc.abs_bound(host(A), orc.dequantize(host(q), host(s)))
+    assert np.all(np.abs(outs[0].astype(np.float64) - row) <= 1e-4 * bound)
+
+
+def test_packed_k_zero():
+    n = 32
+    C = torch.full((2, n), 3.0, device="cuda")
+    A = torch.empty((2, 0), device="cuda")
+    packed = torch.empty((0,), dtype=torch.int8, device="cuda")
+    s = torch.ones((n,), device="cuda")
+    em.matmul_packed(A, packed, n, s, C, accumulate=True)
+    assert np.all(host(C) == 3.0)
+    em.matmul_packed(A, packed, n, s, C)
+    assert np.all(host(C) == 0.0)
+
+
+def test_packed_graph_replay_matches_eager():
+    m, k, n = 1, 4096, 1024
+    A = dev(inputs.normal((m, k), 1.0, 41))
+    q, s = em.quantize_q8(dev(inputs.normal((k, n), 0.02, 42)))
+    packed = em.pack_q8(q)
+    C = torch.empty((m, n), device="cuda")
+    em.matmul_packed(A, packed, n, s, C)
+    eager = host(C).copy()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        em.matmul_packed(A, packed, n, s, C)
+    for _ in range(3):
+        C.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        assert np.array_equal(host(C), eager)
