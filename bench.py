@@ -52,9 +52,12 @@ BF16_MFMA_PEAK_TFLOPS = 2516.6   # MI355X dense bf16 (no sparsity)
 EXACT_SPLIT_PEAK_TFLOPS = BF16_MFMA_PEAK_TFLOPS / 3
 
 
-def q8_kernel(m: int) -> tuple:
-    """(kernel name, compute peak in TFLOP/s) that automatic uses for int8 B."""
-    if m <= 8:
+def q8_kernel(m: int, k: int = 4096, n: int = 4096) -> tuple:
+    """(kernel name, compute peak in TFLOP/s) that automatic uses for int8 B
+    (row-major, unregistered): the GEMV up to 4 rows of small weights, the
+    exact-split kernel from 5 rows (split_bf16_preferred)."""
+    w = k * n
+    if m < 5 and not (m >= 3 and w >= 1 << 25) and not (m >= 2 and w >= 1 << 26):
         return "skinny GEMV (fp32 VALU)", FP32_MFMA_PEAK_TFLOPS / 2
     return "exact-split bf16 MFMA (3 terms)", EXACT_SPLIT_PEAK_TFLOPS
 METRIC = "int8 GEMV HBM GB/s (m=1, 4096²) + fp32 GEMM TFLOPS (N=4096), % of peak"
@@ -77,13 +80,18 @@ def gemv_bytes(m: int, k: int, n: int, q8: bool) -> int:
 
 
 class Pool:
-    """POOL copies of a K x N weight matrix (int8 + scales, or fp32) on the GPU;
-    with packed, int8 copies are kept in the strip layout (em_pack_q8) only."""
+    """POOL copies of a K x N weight matrix (int8 + scales, or fp32) on the GPU.
+    With packed, int8 copies are kept in the strip layout (em_pack_q8) only;
+    with register, each row-major int8 copy is registered with the library
+    (em_q8_register, what the C++ DeviceQTensor does when it is built), so
+    em_matmul_q8 runs one-row products over its strip copy."""
 
     def __init__(self, em, torch, q8: bool, k: int, n: int, copies: int, seed: int,
-                 packed: bool = False):
+                 packed: bool = False, register: bool = False):
         self.q8 = q8
         self.packed = packed
+        self.em = em
+        self.registered = []
         self.ws, self.scales = [], []
         g = torch.Generator(device="cuda")
         for i in range(copies):
@@ -95,6 +103,9 @@ class Pool:
                     pq = em.pack_q8(q)
                     del q
                     q = pq
+                elif register:
+                    em.register_q8(q)
+                    self.registered.append(q)
                 self.ws.append(q)
                 self.scales.append(s)
                 del W
@@ -102,6 +113,15 @@ class Pool:
                 self.ws.append(W)
                 self.scales.append(None)
         torch.cuda.synchronize()
+
+    def close(self):
+        for q in self.registered:
+            self.em.unregister_q8(q)
+        self.registered = []
+        self.ws, self.scales = [], []
+
+    def __del__(self):
+        self.close()
 
 
 def pool_product(em, A, C, pool, w, s):
@@ -145,10 +165,10 @@ def time_graph(torch, graph, steps: int, warmup: int):
 
 
 def gemv_case(em, torch, m, q8, steps, warmup, copies=None, seed=1000, k=DIM, n=DIM,
-              packed=False):
+              packed=False, register=False):
     per_copy = k * n * (1 if q8 else 4)
     copies = copies or max(2, -(-POOL_MIN_BYTES // per_copy))
-    pool = Pool(em, torch, q8, k, n, copies, seed, packed=packed)
+    pool = Pool(em, torch, q8, k, n, copies, seed, packed=packed, register=register)
     g = torch.Generator(device="cuda")
     g.manual_seed(7 + m)
     A = torch.randn((m, k), generator=g, device="cuda", dtype=torch.float32)
@@ -161,7 +181,9 @@ def gemv_case(em, torch, m, q8, steps, warmup, copies=None, seed=1000, k=DIM, n=
            "calls": calls, "us_per_call": secs / calls * 1e6,
            "GBps": nbytes * calls / secs / 1e9, "bytes_per_call": nbytes,
            "wall_s": wall, "secs": secs, "flops_per_call": 2 * m * k * n}
-    del graph, pool
+    del graph
+    pool.close()
+    del pool
     torch.cuda.synchronize()
     return out, (A, C)
 
@@ -310,11 +332,13 @@ def stories15m_case(em, torch, steps: int = 98):
 
 def llama7b_case(em, torch, steps):
     """Per-projection and whole-layer times at decode (m = 1, cache-cold
-    rotating pools, graph replay) and prefill (m = 512, events over reps)."""
+    rotating pools of registered weights, graph replay) and prefill (m = 512,
+    events over reps)."""
     out = {"decode_m1": {}, "prefill_m512": {}}
     times1, times512 = {}, {}
     for k, n in sorted({(k, n) for _, k, n in LLAMA7B_LAYER} | {(4096, 32000)}):
-        r, _ = gemv_case(em, torch, 1, True, max(4, steps // 4), 2, seed=50, k=k, n=n)
+        r, _ = gemv_case(em, torch, 1, True, max(4, steps // 4), 2, seed=50, k=k, n=n,
+                         register=True)
         times1[(k, n)] = r["us_per_call"]
         W = torch.randn((k, n), device="cuda") * 0.02
         q, s = em.quantize_q8(W)
@@ -387,6 +411,40 @@ def gemm_case(em, torch, N=4096, reps=50, warmup=40):
     tflops = 2 * N**3 / secs / 1e12
     return {"N": N, "ms": secs * 1e3, "TFLOPS": tflops,
             "pct_of_fp32_mfma_peak": 100 * tflops / FP32_MFMA_PEAK_TFLOPS}, (A, B)
+
+
+def vendor_gemm_case(em, torch, reps: int = 20, warmup: int = 10) -> dict:
+    """The reference bench's yardstick column (bench_cuda.cpp:58-64,93-110,
+    cuBLAS sgemm there): ROCm's fp32 GEMM through torch.mm (hipBLASLt /
+    rocBLAS, full fp32: TF32-style reduced precision switched off) beside the
+    library's tiled kernel, N = 1024 / 2048 / 4096, same inputs, HIP events."""
+    torch.backends.cuda.matmul.allow_tf32 = False
+    out = {}
+    for N in (1024, 2048, 4096):
+        g = torch.Generator(device="cuda")
+        g.manual_seed(3)
+        A = torch.rand((N, N), generator=g, device="cuda") * 2 - 1
+        B = torch.rand((N, N), generator=g, device="cuda") * 2 - 1
+        C = torch.empty((N, N), device="cuda")
+        row = {}
+        for name, fn in (("tiled", lambda: em.matmul(A, B, C, kernel="tiled")),
+                         ("vendor_torch_mm", lambda: torch.mm(A, B, out=C))):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / reps
+            row[name] = {"ms": round(ms, 4), "TFLOPS": round(2 * N**3 / ms / 1e9, 2)}
+        row["tiled_over_vendor"] = round(row["tiled"]["TFLOPS"] / row["vendor_torch_mm"]["TFLOPS"], 3)
+        out[f"N{N}"] = row
+        del A, B, C
+    torch.cuda.synchronize()
+    return out
 
 
 CALIBRATION_BYTES = 256 << 20
@@ -649,6 +707,34 @@ def floor_study(em, torch, reps: int = 20) -> dict:
     return out
 
 
+def single_launch_floor(em, torch, reps: int = 20) -> dict:
+    """The headline call's floors, with its method (graph replay over 38
+    rotating 16 MiB copies): an empty launch, and one launch reading a whole
+    copy (em_probe_read, the two best shapes of bench.py --floor)."""
+    copies = 38
+    g = graph_of(torch, lambda i: em.probe_empty(256), 2 * copies)
+    secs, _ = time_graph(torch, g, reps, 3)
+    del g
+    out = {"empty_us": round(secs / (reps * 2 * copies) * 1e6, 3)}
+    mib16 = 16 << 20
+    bufs = [torch.randint(-127, 128, (mib16,), dtype=torch.int8, device="cuda")
+            for _ in range(copies)]
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    best = None
+    for blocks, depth, contig in ((256, 16, True), (512, 8, False)):
+        g = graph_of(torch, lambda i, b=blocks, d=depth, c=contig:
+                     em.probe_read(bufs[i % copies], sink, b, d, c), copies)
+        secs, _ = time_graph(torch, g, reps, 3)
+        del g
+        us = secs / (reps * copies) * 1e6
+        best = us if best is None else min(best, us)
+    out["read16_us"] = round(best, 3)
+    out["read16_GBps"] = round(mib16 / best / 1e3, 1)
+    del bufs
+    torch.cuda.synchronize()
+    return out
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -660,12 +746,7 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_threads() -> int:
-    try:
-        n = len(os.sched_getaffinity(0))
-    except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(16, n))
+
 
 
 def cpu_baseline(A_dev, q_dev, s_dev, gemm_AB):
@@ -675,7 +756,7 @@ def cpu_baseline(A_dev, q_dev, s_dev, gemm_AB):
     ref = oracle.ref()
     if ref is None:
         return None
-    threads = cpu_threads()
+    threads = 0  # the reference's default pool (hardware_concurrency, thread_pool.cpp)
     A = A_dev.cpu().numpy()
     q = q_dev.cpu().numpy()
     s = s_dev.cpu().numpy()
@@ -684,7 +765,8 @@ def cpu_baseline(A_dev, q_dev, s_dev, gemm_AB):
     reps = int(max(15, min(2001, 3.0 / max(one, 1e-6)))) | 1
     secs = ref.time_parallel_q8(A, q, s, reps, threads)
     nbytes = gemv_bytes(A.shape[0], q.shape[0], q.shape[1], True)
-    out = {"value": nbytes / secs / 1e9, "unit": "GB/s", "cores": threads, "kind": "reference",
+    out = {"value": nbytes / secs / 1e9, "unit": "GB/s", "cores": ref.pool_size(),
+           "kind": "reference",
            "sample": f"int8 GEMV m=1 4096x4096 (one W, no rotation), matmul_parallel, "
                      f"median of {reps} reps after 1 warm-up",
            "ms": secs * 1e3, "compiler": ref.compiler().split("(")[0].strip(),
@@ -767,13 +849,17 @@ def main() -> int:
         print(json.dumps(profile_pass(em, torch)))
         return 0
 
-    head, (A1, _) = gemv_case(em, torch, 1, True, args.steps, args.warmup)
+    head, (A1, _) = gemv_case(em, torch, 1, True, args.steps, args.warmup, register=True)
+    progress("headline done")
+    rowmajor, _ = gemv_case(em, torch, 1, True, max(5, args.steps // 2), 2)
+    floor = single_launch_floor(em, torch)
     ceiling = hbm_ceiling(em, torch)
     steps = args.steps
     secs = head["secs"]
     avg_launch_s = secs / head["calls"]
     achieved = head["bytes_per_call"] / avg_launch_s / 1e9
     traffic = measured_traffic()
+    read16 = floor["read16_GBps"]
     result = {
         "metric": METRIC,
         "value": round(head["GBps"], 1),
@@ -788,32 +874,48 @@ def main() -> int:
         "dtype": "f32 (int8 weights widened to fp32; fp32 accumulate)",
         "data": "synthetic: A ~ N(0,1), W ~ N(0,0.02) quantised on the GPU (bit-exact quant.cpp)",
         "config": {"workload": "int8 GEMV m=1, A[1,4096] x Wq[4096,4096] + fp32 scales "
-                               "(BASELINE configs[1]); one step = one sweep over "
+                               "(BASELINE configs[1]) through em_matmul_q8 (matmul_cuda's int8 "
+                               "overload) on row-major weights registered at load time "
+                               "(em_q8_register, as DeviceQTensor's constructor does: the library "
+                               "keeps a strip-layout copy and runs the one-row product in one "
+                               "launch); one step = one sweep over "
                                f"{head['copies']} weight copies ({head['pool_MiB']} MiB), "
                                "HIP-graph replay",
                    "m": 1, "k": DIM, "n": DIM, "weight_pool_copies": head["copies"],
-                   "pct_of_hbm_peak": round(100 * head["GBps"] / HBM_PEAK_GBS, 2)},
+                   "pct_of_hbm_peak": round(100 * head["GBps"] / HBM_PEAK_GBS, 2),
+                   "unregistered_rowmajor": {
+                       "us_per_call": round(rowmajor["us_per_call"], 3),
+                       "GBps": round(rowmajor["GBps"], 1),
+                       "kernel": "gemv_kernel<int8,1,16,16> + reduce_slices (split-K, two "
+                                 "launches)"}},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic["hbm_bytes_per_call"] if traffic else None,
                      "traffic_note": (traffic["note"] if traffic else
                                       "no counter summary in profiles/"),
-                     "kernel": "gemv_kernel<int8,1,16,16> + reduce_slices (one em_matmul_q8 call: "
-                               "split-K partials, then the fixed-order slice sum)",
+                     "kernel": "gemv_packed_kernel<256,1,16> (one em_matmul_q8 call over a "
+                               "registered matrix: one launch, no split-K partials)",
                      "avg_launch_us": round(avg_launch_s * 1e6, 3),
                      "bytes_per_launch": head["bytes_per_call"],
+                     "single_launch_floor_GBps": read16,
+                     "frac_of_single_launch_floor": round(achieved / read16, 4),
+                     "floor_note": "em_probe_read of one 16 MiB pool copy per launch over 38 "
+                                   "copies, graph replay, same run (best of contiguous 256 x 16 "
+                                   "and strided 512 x 8): the fastest any one launch reads the "
+                                   f"call's bytes; empty launch {floor['empty_us']} us",
                      "achievable_read_GBps": ceiling["read_stream_GBps"],
                      "frac_of_achievable": round(achieved / ceiling["read_stream_GBps"], 4),
-                     "achievable_note": "em_stream_read over a 600 MiB buffer in the same run "
-                                        "(device-to-device copy: "
-                                        f"{ceiling['d2d_copy_GBps']} GB/s read + write)"},
+                     "achievable_note": "em_stream_read (1024 workgroups, 16 loads in flight, "
+                                        "contiguous chunks) over a 600 MiB buffer, same run; "
+                                        "device-to-device copy "
+                                        f"{ceiling['d2d_copy_GBps']} GB/s read + write"},
     }
 
     extra = {}
     q_keep = None
     gemm_AB = None
     if not args.no_extra:
-        for m in (4, 16, 64):
+        for m in (4, 8, 16, 32, 64):  # bench_cuda.cpp:112-144's decode rows
             r, _ = gemv_case(em, torch, m, True, max(5, steps // 2), 2)
             kname, peak = q8_kernel(m)
             t_mfma = r["flops_per_call"] / (peak * 1e12)
@@ -830,6 +932,7 @@ def main() -> int:
         gemm, gemm_AB = gemm_case(em, torch)
         extra["fp32_gemm_N4096"] = {k: round(v, 3) if isinstance(v, float) else v
                                     for k, v in gemm.items()}
+        extra["fp32_gemm_vendor"] = vendor_gemm_case(em, torch)
         progress("gemv and gemm legs done")
         extra["llama7b_layer_int8"] = llama7b_case(em, torch, steps)
         progress("llama7b layer done")

@@ -93,7 +93,8 @@ private:
 };
 
 // int8 matrix plus one fp32 scale per column in GPU memory, as QTensor.
-// Move-only (cuda_matmul.h:42-64).
+// Move-only (cuda_matmul.h:42-64). Also registers a strip-layout copy of its
+// bytes with the library (em_q8_register; EM_STRIP_COPY=0 turns it off).
 class DeviceQTensor {
 public:
     DeviceQTensor() = default;
@@ -110,13 +111,19 @@ public:
             if (!t.scale.empty())
                 em_detail::check(
                     em_memcpy_h2d(scale_, t.scale.data(), t.scale.size() * sizeof(float)));
+            // The library's strip copy of the bytes (em_q8_register): one-row
+            // products over this matrix then run in one launch. The bytes are
+            // never written again, so the copy stays valid.
+            em_detail::check(em_q8_register(data_, rows_, cols_, EM_STREAM_PER_THREAD));
         } catch (...) {
+            em_q8_unregister(data_);
             em_free(data_);
             em_free(scale_);
             throw;
         }
     }
     ~DeviceQTensor() {
+        em_q8_unregister(data_);
         em_free(data_);
         em_free(scale_);
     }

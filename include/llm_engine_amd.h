@@ -99,6 +99,23 @@ int em_matmul_q8(size_t m, size_t n, size_t k, const float* A, const int8_t* B,
  * buffers of k * n bytes. No counterpart in the reference. */
 int em_pack_q8(size_t k, size_t n, const int8_t* B, int8_t* packed, void* stream);
 int em_unpack_q8(size_t k, size_t n, const int8_t* packed, int8_t* B, void* stream);
+/* Registers row-major int8 weights B (k x n, device memory) for em_matmul_q8:
+ * the library keeps a strip-layout copy, packed from B's bytes on `stream`
+ * (then drained), and em_matmul_q8 with EM_KERNEL_AUTOMATIC or
+ * EM_KERNEL_SKINNY runs one-row products (m == 1, k <= 8192) over that copy
+ * in one launch: same semantics, results within the same tolerance of the
+ * row-major path, bit-identical across repeats. B's bytes must not change
+ * while it is registered (register again after changing them); unregister
+ * before freeing B. Registering again replaces the copy. Shapes the layout
+ * cannot hold (n % 16 != 0, misaligned B) and EM_STRIP_COPY=0 in the
+ * environment leave B unregistered (EM_OK). The C++ DeviceQTensor registers
+ * its buffer on construction and unregisters it on destruction, so the
+ * reference's callers (cuda_model.cu:112,167; bench_cuda.cpp:123,139) get
+ * the one-launch product unchanged. No counterpart in the reference. */
+int em_q8_register(const int8_t* B, size_t k, size_t n, void* stream);
+int em_q8_unregister(const int8_t* B);
+/* 1 if B has a strip copy of shape k x n, else 0. */
+int em_q8_registered(const int8_t* B, size_t k, size_t n);
 /* C = A x dequantize(B) (C += if accumulate; A replaced by rmsnorm(A) *
  * rms_weight when given), B in the strip layout: the semantics of
  * em_matmul_q8 for m <= 8 rows, in one launch, bit-identical across repeats.

@@ -31,6 +31,7 @@ EXPORTS = (
     "em_matmul_f32", "em_matmul_q8", "em_quantize_q8", "em_dequantize_q8", "em_stream_read",
     "em_probe_empty", "em_probe_read", "em_probe_gemv_q8",
     "em_pack_q8", "em_unpack_q8", "em_matmul_q8_packed",
+    "em_q8_register", "em_q8_unregister", "em_q8_registered",
     "em_attention_check", "em_attention_scratch_floats", "em_attention",
     "em_model_create", "em_model_destroy", "em_model_forward",
 )
@@ -123,6 +124,9 @@ def lib() -> ctypes.CDLL:
         L.em_unpack_q8.argtypes = [_sz, _sz, _vp, _vp, _vp]
         L.em_matmul_q8_packed.argtypes = [_sz, _sz, _sz, _vp, _vp, _vp, _vp, ctypes.c_int, _vp,
                                           _vp]
+        L.em_q8_register.argtypes = [_vp, _sz, _sz, _vp]
+        L.em_q8_unregister.argtypes = [_vp]
+        L.em_q8_registered.argtypes = [_vp, _sz, _sz]
         L.em_probe_empty.argtypes = [ctypes.c_uint, _vp]
         L.em_probe_read.argtypes = [_vp, _sz, _vp, ctypes.c_uint, ctypes.c_uint, ctypes.c_int, _vp]
         L.em_probe_gemv_q8.argtypes = [_sz, _sz, _sz, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _vp]
@@ -276,6 +280,23 @@ def matmul_packed(A, packed, n: int, scale, C=None, *, accumulate=False, rms_wei
                                      _dev(scale, torch.float32), _dev(C, torch.float32),
                                      int(bool(accumulate)), rw, _stream_ptr(stream)))
     return C
+
+
+def register_q8(q, stream=None) -> None:
+    """em_q8_register: the library keeps a strip-layout copy of row-major int8
+    weights q [k, n]; matmul() over q then runs one-row products in one launch."""
+    import torch
+    k, n = q.shape
+    _check(lib().em_q8_register(_dev(q, torch.int8), k, n, _stream_ptr(stream)))
+
+
+def unregister_q8(q) -> None:
+    _check(lib().em_q8_unregister(q.data_ptr()))
+
+
+def registered_q8(q) -> bool:
+    k, n = q.shape
+    return bool(lib().em_q8_registered(q.data_ptr(), k, n))
 
 
 def probe_empty(blocks: int, stream=None) -> None:

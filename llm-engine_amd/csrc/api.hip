@@ -13,6 +13,7 @@
 #include <mutex>
 #include <string>
 #include <type_traits>
+#include <unordered_map>
 
 #include "internal.hpp"
 #include "llm_engine_amd.h"
@@ -41,6 +42,35 @@ bool too_many(std::size_t a, std::size_t b) {
     return a != 0 && b > kLimit / a;
 }
 
+
+// Strip copies of registered int8 weights (em_q8_register): the row-major
+// buffer's address -> its shape and a copy in the strip layout.
+struct StripCopy {
+    std::size_t k, n;
+    int8_t* packed;
+};
+std::mutex g_strip_mu;
+std::unordered_map<const void*, StripCopy>& strip_copies() {
+    static std::unordered_map<const void*, StripCopy> m;
+    return m;
+}
+
+// The strip copy of B if one is registered for this shape, else null.
+const int8_t* strip_copy_of(const void* B, std::size_t k, std::size_t n) {
+    std::lock_guard<std::mutex> lock(g_strip_mu);
+    const auto it = strip_copies().find(B);
+    if (it == strip_copies().end() || it->second.k != k || it->second.n != n) return nullptr;
+    return it->second.packed;
+}
+
+// One-row products over registered weights run the strip-layout GEMV: one
+// launch and no split-K partials. Up to 8192 rows of B (one batch of a
+// 256-thread workgroup) it beat the row-major split-K call at every width
+// measured (4096^2: 4.8-4.9 against 6.5 us; 4096 x 11008: 10.0 against
+// 11.8; 4096 x 32000: 23.2 against 25.4); at 11008 rows it lost (13.7
+// against 11.6), and from two rows the GEMV's multiply-adds per byte grow
+// with m and the row-major kernels win.
+constexpr std::size_t kStripMaxK = 8192;
 
 template <class BT>
 int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, const BT* B,
@@ -93,6 +123,14 @@ int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, co
         a.accumulate = accumulate != 0;
         a.rms_weight = rms_weight;
         a.stream = s;
+        if (std::is_same<BT, int8_t>::value && kernel == EM_KERNEL_SKINNY && m == 1 &&
+            k <= kStripMaxK) {
+            if (const int8_t* P = strip_copy_of(B, k, n)) {
+                run_gemv_packed(a, P);
+                hip_check(hipGetLastError(), "launch");
+                return EM_OK;
+            }
+        }
         if (std::is_same<BT, int8_t>::value && automatic && split_bf16_preferred(a.m, a.n, a.k) &&
             split_bf16_supports(a)) {
             run_split_bf16(a);  // fuses the norm
@@ -322,6 +360,59 @@ int em_pack_q8(size_t k, size_t n, const int8_t* B, int8_t* packed, void* stream
         return fail(EM_EDEVICE, e.what());
     }
     return EM_OK;
+}
+
+int em_q8_register(const int8_t* B, size_t k, size_t n, void* stream) {
+    if (too_many(k, n)) return fail(EM_EINVAL, "q8_register: more than 2^31 elements");
+    if (k == 0 || n == 0) return EM_OK;
+    if (!B) return fail(EM_EINVAL, "q8_register: null pointer");
+    static const bool enabled = [] {
+        const char* v = std::getenv("EM_STRIP_COPY");
+        return !(v && v[0] == '0');
+    }();
+    // Shapes the strip layout cannot hold are left row-major.
+    if (!enabled || n % 16 || reinterpret_cast<uintptr_t>(B) % 16) return EM_OK;
+    if (!em::device_present()) return fail(EM_ENODEV, "q8_register: no usable GPU");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    try {
+        std::lock_guard<std::mutex> lock(em::g_strip_mu);
+        auto& map = em::strip_copies();
+        auto it = map.find(B);
+        if (it != map.end() && (it->second.k != k || it->second.n != n)) {
+            em::hip_check(hipFree(it->second.packed), "free strip copy");
+            map.erase(it);
+            it = map.end();
+        }
+        if (it == map.end()) {
+            void* p = nullptr;
+            em::hip_check(hipMalloc(&p, k * n), "alloc strip copy");
+            it = map.emplace(B, em::StripCopy{k, n, static_cast<int8_t*>(p)}).first;
+        }
+        // Packed (again) from B's current bytes; load-time work, so the
+        // stream is drained before the copy is used on any other stream.
+        em::run_pack_strips(static_cast<int>(k), static_cast<int>(n), B, it->second.packed, s);
+        em::hip_check(hipGetLastError(), "launch");
+        em::hip_check(hipStreamSynchronize(s), "pack strip copy");
+    } catch (const std::exception& e) {
+        return fail(EM_EDEVICE, e.what());
+    }
+    return EM_OK;
+}
+
+int em_q8_unregister(const int8_t* B) {
+    std::lock_guard<std::mutex> lock(em::g_strip_mu);
+    auto& map = em::strip_copies();
+    const auto it = map.find(B);
+    if (it == map.end()) return EM_OK;
+    const hipError_t err = hipFree(it->second.packed);  // waits for queued work
+    map.erase(it);
+    if (err != hipSuccess)
+        return fail(EM_EDEVICE, std::string("hip: free strip copy: ") + hipGetErrorString(err));
+    return EM_OK;
+}
+
+int em_q8_registered(const int8_t* B, size_t k, size_t n) {
+    return em::strip_copy_of(B, k, n) ? 1 : 0;
 }
 
 int em_unpack_q8(size_t k, size_t n, const int8_t* packed, int8_t* B, void* stream) {

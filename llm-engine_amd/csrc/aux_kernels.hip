@@ -12,9 +12,10 @@
 //                   inv = 1 / scale with IEEE division, then
 //                   q = clamp(round-half-away(B * inv), -127, 127)
 //   dequantize_q8   quant.cpp:30-36
-//   stream_read     a read-only pass over a buffer: the HBM ceiling that the
-//                   GEMV is compared with (no counterpart in the reference,
-//                   whose bench times a device-to-device copy instead,
+//   stream_read     a read-only pass over a buffer (probes.hip's read kernel
+//                   in its fastest shape): the HBM ceiling that the GEMV is
+//                   compared with (no counterpart in the reference, whose
+//                   bench times a device-to-device copy instead,
 //                   bench_cuda.cpp:79-88)
 #include <algorithm>
 #include <type_traits>
@@ -70,28 +71,6 @@ __global__ __launch_bounds__(kThreads) void reduce_slices_kernel(
         const float sq = wave_sum(in ? out * out : 0.0f);
         if (in && threadIdx.x % kWave == 0) ssq[i / kSsqChunk] = sq;
     }
-}
-
-// Eight nontemporal 16-byte loads in flight per thread per step, folded
-// into an xor so that none is dead; the one store is taken only if the xor
-// hits a fixed value (about never), so nothing but the loads reaches memory.
-__global__ __launch_bounds__(kThreads) void stream_read_kernel(const uint4* p, size_t n16,
-                                                               uint32_t* sink) {
-    const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
-    size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
-    uint32_t acc = 0;
-    for (; i + 7 * stride < n16; i += 8 * stride) {
-        uint4 v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = stream_load(p + i + u * stride);
-#pragma unroll
-        for (int u = 0; u < 8; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
-    }
-    for (; i < n16; i += stride) {
-        const uint4 v = stream_load(p + i);
-        acc ^= v.x ^ v.y ^ v.z ^ v.w;
-    }
-    if (acc == 0x9e3779b9u) *sink = acc;
 }
 
 __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(int k, const float* A,
@@ -246,12 +225,15 @@ void run_reduce_slices(int m, int n, int slices, const float* partial, const flo
                        n % kSsqChunk == 0 ? ssq : nullptr);
 }
 
+// The read ceiling: 1024 workgroups, 16 loads in flight per thread, each
+// workgroup on one contiguous chunk -- the fastest shape of the floor
+// study's sweep over a 600 MiB buffer (6.95-6.98 TB/s against 5.1-5.4 for
+// a 2048-workgroup grid stride with 8 loads in flight).
 void run_stream_read(const void* buf, std::size_t bytes, uint32_t* sink, hipStream_t stream) {
-    const std::size_t n16 = bytes / 16;
-    const int blocks = static_cast<int>(std::min<std::size_t>(
-        static_cast<std::size_t>(cu_count()) * 8, (n16 + kThreads - 1) / kThreads));
-    hipLaunchKernelGGL(stream_read_kernel, dim3(std::max(blocks, 1)), dim3(kThreads), 0, stream,
-                       static_cast<const uint4*>(buf), n16, sink);
+    const std::size_t per = static_cast<std::size_t>(kThreads) * 16 * 16;
+    const int blocks = static_cast<int>(std::max<std::size_t>(
+        1, std::min<std::size_t>(1024, (bytes + per - 1) / per)));
+    run_probe_read(buf, bytes, blocks, 16, true, sink, stream);
 }
 
 void run_rmsnorm_rows(int m, int k, const float* A, const float* w, float* out,

@@ -73,6 +73,21 @@ __device__ __forceinline__ float block_sum(float v, float* part) {
     return (part[0] + part[1]) + (part[2] + part[3]);
 }
 
+// Halving steps of a cross-lane reduce-scatter (gfx950 lane swaps, no LDS).
+// fold32(x, y): lanes 0-31 get x + x of lane + 32, lanes 32-63 get y of lane
+// - 32 + y; fold16(x, y): the same between rows of 16 (even rows x, odd rows
+// y). Each sum is formed in exactly one lane, so the result is fixed.
+__device__ __forceinline__ float fold32(float x, float y) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false,
+                                                    false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float fold16(float x, float y) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false,
+                                                    false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Four int8 in one 32-bit word, widened to fp32. hipcc turns each into one
 // v_cvt_f32_i32 with an SDWA sign-extended byte select.
 __device__ __forceinline__ void widen4(uint32_t w, float* out) {

@@ -158,7 +158,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
     constexpr bool kQ8 = std::is_same<BT, int8_t>::value;
 
     __shared__ float a_s[MM * R];
-    __shared__ float red[E * E * RS];
+    // E == 16: the four waves' column sums (after the in-wave fold), else
+    // every row group's sums.
+    __shared__ float red[E == 16 ? MM * 4 * kThreads : E * E * RS];
     __shared__ float part[4];
     __shared__ float rs_s[MM];
 
@@ -422,16 +424,46 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
     // owns local column t of the tile. Rows past m hold zeros and go through
     // the same steps with their stores skipped: a branch on m around the
     // barriers measured 0.6 us slower per 16 MiB GEMV.
+    //
+    // With 16 columns per lane (16 lanes a row), the four row groups of a
+    // wave are lanes l, l ^ 16, l ^ 32, l ^ 48: two lane-swap folds leave
+    // each lane four sums of consecutive columns (16 cg + 4 b4 + 8 b5 + i,
+    // b4 and b5 the lane's bits 4 and 5), written as one 16-byte store; one
+    // barrier, then thread t adds the four waves' sums of column t in wave
+    // order. Other widths add every row group's sums through LDS.
     const int ccg = tid / E, cj = tid % E;
     const int c = blockIdx.x * kThreads + tid;
+    if constexpr (E == 16) {
+        const int lane = tid % kWave, wave = tid / kWave;
+#pragma unroll
+        for (int r = 0; r < MM; ++r) {
+            float a8[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a8[i] = fold32(acc[r][i], acc[r][i + 8]);
+            float4 a4;
+            a4.x = fold16(a8[0], a8[4]);
+            a4.y = fold16(a8[1], a8[5]);
+            a4.z = fold16(a8[2], a8[6]);
+            a4.w = fold16(a8[3], a8[7]);
+            const int col = 16 * cg + 4 * ((lane >> 4) & 1) + 8 * ((lane >> 5) & 1);
+            *reinterpret_cast<float4*>(&red[(r * 4 + wave) * kThreads + col]) = a4;
+        }
+        __syncthreads();
+    }
 #pragma unroll
     for (int r = 0; r < MM; ++r) {
-#pragma unroll
-        for (int j = 0; j < E; ++j) red[(rg * E + j) * RS + cg] = acc[r][j];
-        __syncthreads();
         float total = 0.0f;
+        if constexpr (E == 16) {
+            total = red[(r * 4) * kThreads + tid];
 #pragma unroll
-        for (int g = 0; g < E; ++g) total += red[(g * E + cj) * RS + ccg];
+            for (int w = 1; w < 4; ++w) total += red[(r * 4 + w) * kThreads + tid];
+        } else {
+#pragma unroll
+            for (int j = 0; j < E; ++j) red[(rg * E + j) * RS + cg] = acc[r][j];
+            __syncthreads();
+#pragma unroll
+            for (int g = 0; g < E; ++g) total += red[(g * E + cj) * RS + ccg];
+        }
         if (r < p.m && c < p.n) {
             if (p.direct) {
                 float v = total;
@@ -447,13 +479,14 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
                 }
             }
         }
-        __syncthreads();
+        if constexpr (E != 16) __syncthreads();
     }
     if constexpr (ARR != 0) {
         // Every store above happens before thread 0's release (the barrier
         // orders them within the workgroup); the last arrival's acquire then
         // makes all of the tile's partials visible to its threads.
         __shared__ int last_s;
+        __syncthreads();
         if (tid == 0) {
             const int before = __hip_atomic_fetch_add(p.arrive + blockIdx.x, 1, __ATOMIC_ACQ_REL,
                                                       __HIP_MEMORY_SCOPE_AGENT);

@@ -112,18 +112,10 @@ __device__ __forceinline__ float wave_reduce_scatter16(float (&v)[16]) {
     const int lane = threadIdx.x % kWave;
     float a8[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]),
-                                                        __float_as_uint(v[i + 8]), false, false);
-        a8[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
+    for (int i = 0; i < 8; ++i) a8[i] = fold32(v[i], v[i + 8]);
     float a4[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a8[i]),
-                                                        __float_as_uint(a8[i + 4]), false, false);
-        a4[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
+    for (int i = 0; i < 4; ++i) a4[i] = fold16(a8[i], a8[i + 4]);
     // DPP reads a lane that is switched off as zero, so both sides of each
     // choice are formed by every lane (outside any branch), then selected.
     const bool b3 = lane & 8, b2 = lane & 4;
@@ -339,9 +331,10 @@ void launch_depth(int L, const PackedParams& p, hipStream_t s) {
     auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(NT), 0, s, p); };
     if (L > LMAX) L = LMAX;
     if (NT * L < p.k) {
-        // Several batches, half as deep, so the next batch's loads fit
-        // beside this one's.
-        constexpr int LM = LMAX >= 8 ? LMAX / 2 : LMAX;
+        // Several batches, half as deep (at most 8 rows a lane from 512
+        // threads up), so the next batch's loads fit beside this one's.
+        constexpr int LH = LMAX >= 8 ? LMAX / 2 : LMAX;
+        constexpr int LM = NT >= 512 && LH > 8 ? 8 : LH;
         return go(gemv_packed_kernel<NT, MM, LM, NORM, VEC, true>);
     }
     if (L <= 4) return go(gemv_packed_kernel<NT, MM, 4, NORM, VEC, false>);
@@ -369,6 +362,10 @@ int packed_depth(int nt, int k, int lmax) {
 template <bool NORM, bool VEC>
 void launch_threads(const PackedParams& p, hipStream_t s) {
     if (p.m <= 1) {
+        // Past 8192 rows a 256-thread workgroup would loop over batches;
+        // 512 threads hold up to 16384 rows in one batch.
+        if (p.k > kThreads * 32 && p.k <= 512 * 32 && packed_threads() == 256)
+            return launch_depth<512, 1, NORM, VEC, 32>(packed_depth(512, p.k, 32), p, s);
         switch (packed_threads()) {
             case 1024:
                 return launch_depth<1024, 1, NORM, VEC, 8>(packed_depth(1024, p.k, 8), p, s);

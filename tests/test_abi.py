@@ -185,3 +185,19 @@ def test_probes_check_before_the_gpu():
     assert L.em_probe_read(16, 64, 16, 0, 8, 0, None) == em.EM_EINVAL
     assert L.em_probe_gemv_q8(2, 16, 16, 16, 16, 16, 16, 0, None, None) == em.EM_EINVAL
     assert L.em_probe_gemv_q8(1, 16, 16, 16, 16, 16, 16, 1, None, None) == em.EM_EINVAL
+
+
+def test_q8_register_checks_before_the_gpu():
+    L = em.lib()
+    assert L.em_q8_register(None, 4, 16, None) == em.EM_EINVAL
+    assert L.em_q8_register(None, 0, 16, None) == em.EM_OK
+    assert L.em_q8_register(16, 1 << 16, 1 << 16, None) == em.EM_EINVAL
+    # A shape the strip layout cannot hold stays row-major: nothing registered.
+    assert L.em_q8_register(16, 4, 20, None) == em.EM_OK
+    assert L.em_q8_registered(16, 4, 20) == 0
+    assert L.em_q8_register(8, 4, 16, None) == em.EM_OK
+    assert L.em_q8_registered(8, 4, 16) == 0
+    # A shape it can hold needs the GPU.
+    assert L.em_q8_register(16, 4, 16, None) == em.EM_ENODEV
+    assert L.em_q8_registered(16, 4, 16) == 0
+    assert L.em_q8_unregister(16) == em.EM_OK

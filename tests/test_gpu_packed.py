@@ -129,3 +129,117 @@ def test_packed_graph_replay_matches_eager():
         torch.cuda.synchronize()
         g.replay()
         assert np.array_equal(host(C), eager)
+
+
+# ---- registered weights: em_matmul_q8 over the strip copy -------------------
+
+REG_SHAPES = [(288, 864), (4096, 4096), (8192, 64), (768, 288), (288, 32000), (17, 48)]
+
+
+@pytest.mark.parametrize("kernel", ["automatic", "skinny"])
+@pytest.mark.parametrize("fusion", ["plain", "acc", "rms", "rms_acc"])
+@pytest.mark.parametrize("shape", REG_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_registered_one_row_against_oracle(shape, fusion, kernel):
+    k, n = shape
+    A = inputs.uniform((1, k), -1.0, 1.0, 51)
+    q, s = orc.quantize_q8(inputs.normal((k, n), 0.02, 52))
+    acc = "acc" in fusion
+    rms = "rms" in fusion
+    C0 = inputs.uniform((1, n), -1.0, 1.0, 53) if acc else None
+    w = inputs.uniform((k,), 0.5, 1.5, 54) if rms else None
+    qd, sd = dev(q), dev(s)
+    em.register_q8(qd)
+    try:
+        assert em.registered_q8(qd)
+        C = dev(C0) if acc else torch.empty((1, n), device="cuda")
+        wd = dev(w) if rms else None
+        em.matmul(dev(A), qd, C, scale=sd, kernel=kernel, accumulate=acc, rms_weight=wd)
+        got = host(C)
+        # The registered call is the strip-layout product, bit for bit.
+        P = em.pack_q8(qd)
+        C2 = dev(C0) if acc else torch.empty((1, n), device="cuda")
+        em.matmul_packed(dev(A), P, n, sd, C2, accumulate=acc, rms_weight=wd)
+        assert np.array_equal(got, host(C2))
+    finally:
+        em.unregister_q8(qd)
+    assert not em.registered_q8(qd)
+    want = orc.matmul_fused(A, Bq=q, scale=s, w=w, C0=C0)
+    An = orc.rmsnorm(A, w) if rms else A
+    check(got, want, An, orc.dequantize(q, s), k, 2.0 if (acc or rms) else 1.0, C0)
+
+
+def test_registered_weights_leave_other_calls_row_major():
+    # More than one row, an explicit MFMA kernel, k past the strip cut and an
+    # unregistered B all run the row-major kernels: the same bits as before
+    # registering.
+    k, n = 4096, 512
+    q, s = em.quantize_q8(dev(inputs.normal((k, n), 0.02, 61)))
+    A1 = dev(inputs.normal((1, k), 1.0, 62))
+    A4 = dev(inputs.normal((4, k), 1.0, 63))
+    before = {name: host(em.matmul(A, q, scale=s, kernel=kern)).copy()
+              for name, A, kern in (("m4", A4, "automatic"), ("tiled", A1, "tiled"),
+                                    ("naive", A1, "naive"))}
+    row1 = host(em.matmul(A1, q, scale=s)).copy()
+    em.register_q8(q)
+    try:
+        for name, A, kern in (("m4", A4, "automatic"), ("tiled", A1, "tiled"),
+                              ("naive", A1, "naive")):
+            assert np.array_equal(host(em.matmul(A, q, scale=s, kernel=kern)), before[name])
+        reg1 = host(em.matmul(A1, q, scale=s)).copy()
+    finally:
+        em.unregister_q8(q)
+    assert np.array_equal(host(em.matmul(A1, q, scale=s)), row1)
+    bound = orc.abs_bound(host(A1), orc.dequantize(host(q), host(s)))
+    assert np.all(np.abs(reg1.astype(np.float64) - row1) <= 1e-4 * bound)
+    # k = 8193: past the strip cut, registered or not the row-major path.
+    q2, s2 = em.quantize_q8(dev(inputs.normal((8193, 64), 0.02, 64)))
+    A2 = dev(inputs.normal((1, 8193), 1.0, 65))
+    want = host(em.matmul(A2, q2, scale=s2)).copy()
+    em.register_q8(q2)
+    try:
+        assert np.array_equal(host(em.matmul(A2, q2, scale=s2)), want)
+    finally:
+        em.unregister_q8(q2)
+
+
+def test_register_again_after_the_bytes_change():
+    k, n = 1024, 256
+    qa, s = em.quantize_q8(dev(inputs.normal((k, n), 0.02, 71)))
+    qb, _ = em.quantize_q8(dev(inputs.normal((k, n), 0.02, 72)))
+    A = dev(inputs.normal((1, k), 1.0, 73))
+    q = qa.clone()
+    em.register_q8(q)
+    try:
+        first = host(em.matmul(A, q, scale=s)).copy()
+        q.copy_(qb)
+        em.register_q8(q)  # repacks from the new bytes
+        second = host(em.matmul(A, q, scale=s)).copy()
+    finally:
+        em.unregister_q8(q)
+    assert np.array_equal(first, host(em.matmul_packed(A, em.pack_q8(qa), n, s)))
+    assert np.array_equal(second, host(em.matmul_packed(A, em.pack_q8(qb), n, s)))
+
+
+def test_registered_graph_replay_matches_eager():
+    k, n = 4096, 2048
+    q, s = em.quantize_q8(dev(inputs.normal((k, n), 0.02, 81)))
+    A = dev(inputs.normal((1, k), 1.0, 82))
+    em.register_q8(q)
+    try:
+        C = torch.empty((1, n), device="cuda")
+        em.matmul(A, q, C, scale=s)
+        eager = host(C).copy()
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            em.matmul(A, q, C, scale=s)
+        for _ in range(3):
+            C.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            assert np.array_equal(host(C), eager)
+        del g
+        torch.cuda.synchronize()
+    finally:
+        em.unregister_q8(q)
