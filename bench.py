@@ -455,7 +455,9 @@ def profile_pass(em, torch, sweeps: int = 2) -> dict:
     passes. First a plain elementwise copy of CALIBRATION_BYTES (torch.neg into
     a second buffer: that many bytes read and as many written, each once), the
     yardstick the HBM byte counters are scaled by; then the headline product
-    (int8 m = 1, 4096^2) over the rotating pool, `sweeps` times."""
+    (int8 m = 1, 4096^2) over the rotating pool, `sweeps` times with the pool
+    registered (the bench's value: gemv_packed_kernel), then `sweeps` times
+    unregistered (row-major: gemv_kernel + reduce_slices)."""
     src = torch.randn(CALIBRATION_BYTES // 4, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -464,15 +466,40 @@ def profile_pass(em, torch, sweeps: int = 2) -> dict:
     del src, dst
     per_copy = DIM * DIM
     copies = -(-POOL_MIN_BYTES // per_copy)
-    pool = Pool(em, torch, True, DIM, DIM, copies, 1000)
+    pool = Pool(em, torch, True, DIM, DIM, copies, 1000, register=True)
     A = torch.randn((1, DIM), device="cuda")
     C = torch.empty((1, DIM), device="cuda")
     for _ in range(sweeps):
         for w, s in zip(pool.ws, pool.scales):
             em.matmul(A, w, C, scale=s)
     torch.cuda.synchronize()
-    return {"calibration_bytes": CALIBRATION_BYTES, "products": sweeps * copies,
+    for q in pool.registered:
+        em.unregister_q8(q)
+    pool.registered = []
+    for _ in range(sweeps):
+        for w, s in zip(pool.ws, pool.scales):
+            em.matmul(A, w, C, scale=s)
+    torch.cuda.synchronize()
+    pool.close()
+    return {"calibration_bytes": CALIBRATION_BYTES, "products": 2 * sweeps * copies,
             "bytes_per_product": gemv_bytes(1, DIM, DIM, True)}
+
+
+def profile_smallm_pass(em, torch, reps: int = 20) -> dict:
+    """Eager int8 products at m = 4, 16 and 64 over the rotating 4096^2 pool
+    (automatic: the GEMV at 4 rows, the exact-split kernel at 16 and 64), for
+    counter passes over the decode-batch kernels."""
+    per_copy = DIM * DIM
+    copies = -(-POOL_MIN_BYTES // per_copy)
+    pool = Pool(em, torch, True, DIM, DIM, copies, 1000)
+    for m in (4, 16, 64):
+        A = torch.randn((m, DIM), device="cuda")
+        C = torch.empty((m, DIM), device="cuda")
+        for i in range(reps):
+            em.matmul(A, pool.ws[i % copies], C, scale=pool.scales[i % copies])
+        torch.cuda.synchronize()
+    pool.close()
+    return {"m": [4, 16, 64], "launches_each": reps}
 
 
 def profile_gemm_pass(em, torch, N: int = 4096, reps: int = 5) -> dict:
@@ -800,7 +827,8 @@ def main() -> int:
     ap.add_argument("--floor", action="store_true",
                     help="only the floor study of the headline call (empty launches, "
                          "16 MiB and 600 MiB read sweeps, single-launch GEMV variants)")
-    ap.add_argument("--profile-pass", nargs="?", const="gemv", choices=["gemv", "gemm", "split", "prefill", "decode"],
+    ap.add_argument("--profile-pass", nargs="?", const="gemv",
+                    choices=["gemv", "gemm", "split", "smallm", "prefill", "decode"],
                     help="eager launches for rocprofv3 --pmc: gemv (calibration copy + "
                          "headline, the default), gemm (fp32 tiled N=4096), split "
                          "(int8 m=512, exact-split), prefill or decode (Llama-7B-shaped, "
@@ -838,6 +866,9 @@ def main() -> int:
         return 0
     if args.profile_pass == "split":
         print(json.dumps(profile_split_pass(em, torch)))
+        return 0
+    if args.profile_pass == "smallm":
+        print(json.dumps(profile_smallm_pass(em, torch)))
         return 0
     if args.profile_pass == "prefill":
         print(json.dumps(profile_prefill_pass(em, torch)))
