@@ -20,6 +20,7 @@
 #include <string>
 #include <vector>
 
+#include "cuda_matmul.h"  // as the reference's header: callers use cuda_available() from it
 #include "llm_engine_amd.h"
 #include "model.h"
 

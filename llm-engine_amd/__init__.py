@@ -86,9 +86,7 @@ def build() -> str:
     spec = importlib.util.spec_from_file_location("_em_build", os.path.join(HERE, "build.py"))
     mod = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(mod)
-    path = mod.build_library()
-    mod.build_cpp_tests()
-    return path
+    return mod.build_library()
 
 
 def lib() -> ctypes.CDLL:

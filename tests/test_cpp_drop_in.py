@@ -1,48 +1,69 @@
-"""Runs the reference's own GPU test programs, restated against this build's
-C++ drop-in headers:
-  tests/cpp/test_drop_in          test_cuda.cpp on cuda_matmul.h / matmul.h /
-                                  quant.h (llm-engine_amd/build.py builds it)
-  tests/cpp/test_cuda_attention   test_cuda_attention.cpp on cuda_attention.h
-                                  (llm-engine_amd/build.py)
-  oracle/_ref/test_cuda_model     test_cuda_model.cpp on cuda_model.h, with the
-                                  reference's CPU Transformer compiled from
-                                  source as the checker (oracle/Makefile e2e)
-Exit 77 means no GPU (skip), as in the reference's CTest setup
-(CMakeLists.txt:112)."""
+"""Runs the reference's own GPU test programs and CPU bench, compiled
+unchanged from /root/reference against this build's drop-in headers by
+oracle/Makefile's e2e target (the built binaries travel in oracle/_ref):
+  oracle/_ref/test_cuda          tests/test_cuda.cpp: every GpuKernel, fusion,
+                                 int8 B, split-K queue and error message, with
+                                 the reference's CPU matmul.cpp as the checker
+  oracle/_ref/test_cuda_model    tests/test_cuda_model.cpp: this build's
+                                 CudaTransformer against the reference's CPU
+                                 Transformer (model.cpp)
+  oracle/_ref/bench_matmul_gpu   bench/bench_matmul.cpp on this build's
+                                 matmul.h / quant.h (the GPU entry points)
+The reference's cuda_attention test and bench_cuda include the CUDA runtime
+and cuBLAS directly, so they cannot be built here; tests/test_gpu_attention.py
+covers attention. Exit 77 means no GPU (skip), as in the reference's CTest
+setup (CMakeLists.txt:112)."""
 import os
 import subprocess
 
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-BINS = {
-    "matmul": os.path.join(ROOT, "tests", "cpp", "test_drop_in"),
-    "attention": os.path.join(ROOT, "tests", "cpp", "test_cuda_attention"),
-    "model": os.path.join(ROOT, "oracle", "_ref", "test_cuda_model"),
+REF_BIN = os.path.join(ROOT, "oracle", "_ref")
+SUITES = {
+    "matmul": os.path.join(REF_BIN, "test_cuda"),
+    "model": os.path.join(REF_BIN, "test_cuda_model"),
 }
+BENCH = os.path.join(REF_BIN, "bench_matmul_gpu")
 
 
-def run(which):
-    path = BINS[which]
+def run(path, *args, timeout=900):
     if not os.path.exists(path):
         pytest.fail(f"{path} is not built (__graft_entry__.build())")
-    return subprocess.run([path], capture_output=True, text=True, timeout=900)
+    return subprocess.run([path, *args], capture_output=True, text=True, timeout=timeout)
 
 
-@pytest.mark.parametrize("which", sorted(BINS))
-def test_binary_links_and_skips_without_gpu(which):
+@pytest.mark.parametrize("which", sorted(SUITES))
+def test_reference_suite_links_and_skips_without_gpu(which):
     import torch
     if torch.cuda.is_available():
         pytest.skip("GPU present: the gpu-marked test runs the suite")
-    r = run(which)
-    assert r.returncode in (0, 77), r.stdout + r.stderr
-    if r.returncode == 77:
-        assert "skipping" in r.stdout
+    r = run(SUITES[which])
+    assert r.returncode == 77, r.stdout + r.stderr
+    assert "skipping" in r.stdout
+
+
+def test_reference_bench_links():
+    out = subprocess.run(["ldd", BENCH], capture_output=True, text=True).stdout
+    assert "libllm_engine_amd.so" in out, out
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("which", sorted(BINS))
+@pytest.mark.parametrize("which", sorted(SUITES))
 def test_reference_gpu_suite_on_drop_in_headers(which):
-    r = run(which)
+    r = run(SUITES[which])
     assert r.returncode == 0, r.stdout + r.stderr
     assert "all tests passed" in r.stdout
+
+
+@pytest.mark.gpu
+def test_reference_bench_matmul_on_the_gpu_entry_points():
+    # bench_matmul.cpp's square table (sizes given: the decode table is
+    # skipped, bench_matmul.cpp:95) through matmul_naive / blocked / parallel.
+    r = run(BENCH, "128", "256", "512", timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    lines = [l for l in r.stdout.splitlines() if l.strip()[:3].strip().isdigit()]
+    assert [int(l.split("|")[0]) for l in lines] == [128, 256, 512], r.stdout
+    for l in lines:
+        cells = [c.split() for c in l.split("|")[1:]]
+        assert all(len(c) == 2 and float(c[1]) > 0 for c in cells), l
