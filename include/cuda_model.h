@@ -47,6 +47,33 @@ public:
     }
     ~CudaTransformer() { em_model_destroy(m_); }
 
+    // load_checkpoint(path) and the constructor in one step, on the GPU
+    // (em_model_load): no CPU-side Checkpoint. std::runtime_error for a file
+    // the reference's loader rejects, with its message. Not in the
+    // reference's class.
+    static CudaTransformer load(const std::string& path, WeightType type = WeightType::f32) {
+        em_model* m = nullptr;
+        const int rc =
+            em_model_load(path.c_str(), type == WeightType::q8 ? EM_WEIGHTS_Q8 : EM_WEIGHTS_F32, &m);
+        if (rc == EM_EINVAL) throw std::invalid_argument(em_last_error());
+        if (rc != EM_OK) throw std::runtime_error(em_last_error());
+        em_model_config c{};
+        em_model_config_get(m, &c);
+        Config cfg{};
+        cfg.dim = c.dim;
+        cfg.hidden_dim = c.hidden_dim;
+        cfg.n_layers = c.n_layers;
+        cfg.n_heads = c.n_heads;
+        cfg.n_kv_heads = c.n_kv_heads;
+        cfg.vocab_size = c.vocab_size;
+        cfg.seq_len = c.seq_len;
+        return CudaTransformer(m, cfg);
+    }
+    CudaTransformer(CudaTransformer&& o) noexcept
+        : cfg_(o.cfg_), m_(o.m_), logits_(std::move(o.logits_)) {
+        o.m_ = nullptr;
+    }
+
     CudaTransformer(const CudaTransformer&) = delete;
     CudaTransformer& operator=(const CudaTransformer&) = delete;
 
@@ -60,6 +87,8 @@ public:
     const Config& config() const { return cfg_; }
 
 private:
+    CudaTransformer(em_model* m, const Config& cfg) : cfg_(cfg), m_(m), logits_(cfg.vocab_size) {}
+
     const std::vector<float>& run(const int* tokens, std::size_t n, std::size_t pos) {
         const int rc = em_model_forward(m_, tokens, n, pos, logits_.data());
         if (rc == EM_ERANGE) throw std::out_of_range(em_last_error());

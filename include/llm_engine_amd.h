@@ -35,6 +35,8 @@ extern "C" {
 #define EM_EDEVICE 2 /* a HIP runtime error (std::runtime_error "cuda: <op>: <err>") */
 #define EM_ENODEV 3  /* no usable GPU */
 #define EM_ERANGE 4  /* a token or position outside the model's range (std::out_of_range) */
+#define EM_EIO 5     /* a checkpoint that cannot be opened or read, or whose header or size is
+                        bad (std::runtime_error from load_checkpoint) */
 
 /* Kernel choice; replaces enum class GpuKernel, cuda_matmul.h:61-67. */
 #define EM_KERNEL_AUTOMATIC 0   /* fp32 B: skinny for m <= 8 (m <= 3 for 2^25 weights or more),
@@ -243,6 +245,35 @@ typedef struct em_model em_model;
 int em_model_create(const em_model_config* cfg, const float* token_embedding,
                     const em_layer_weights* layers, const float* rms_final, const float* wcls,
                     int weight_type, em_model** out);
+
+/* Loads a llama2.c v0 checkpoint from `path` straight into a model: replaces
+ *   Checkpoint load_checkpoint(const std::string& path)     model.h:69-71,
+ *                                                           model.cpp:115-163
+ * followed by CudaTransformer(ckpt, type). The 7-int header is checked as the
+ * reference checks it (every field non-zero, all but the vocabulary
+ * positive; dim split into even-sized heads, whole kv groups) and the file
+ * size against the header; each failure is EM_EIO with the reference's
+ * message ("cannot open checkpoint P", "checkpoint P: bad header field i =
+ * v", "checkpoint P: dim must split ...", "checkpoint P is N bytes, header
+ * implies M", "checkpoint P ended early"). The file streams through pinned
+ * memory to the GPU, which transposes each projection (stored out x in) into
+ * the CPU model's layout, fuses q | k | v and w1 | w3, takes the classifier
+ * from the embedding when the vocabulary is positive, and for EM_WEIGHTS_Q8
+ * quantises with quantize_q8 on the GPU. EM_EINVAL for a shape the forward
+ * pass cannot run (as em_model_create). */
+int em_model_load(const char* path, int weight_type, em_model** out);
+
+/* The model's config (for one from em_model_load, the checkpoint header's). */
+int em_model_config_get(const em_model* m, em_model_config* out);
+
+/* Copies one weight array back to host memory, as stored: "token_embedding",
+ * "rms_final", "wcls", and per layer "rms_att", "wqkv", "wo", "rms_ffn",
+ * "w13", "w2" (the CPU model's Weights / LayerWeights, model.h:29-43) as fp32;
+ * in an int8 model the projections ("wqkv", "wo", "w13", "w2", "wcls") are
+ * their int8 bytes and "<name>.scale" their column scales. `bytes` must be
+ * the array's size (EM_EINVAL otherwise, or for an unknown name). No
+ * counterpart in the reference; for checking a load against the CPU loader. */
+int em_model_read_weight(em_model* m, const char* name, size_t layer, void* dst, size_t bytes);
 
 int em_model_destroy(em_model* m);
 

@@ -20,7 +20,7 @@ from typing import Optional
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libllm_engine_amd.so")
 
-EM_OK, EM_EINVAL, EM_EDEVICE, EM_ENODEV, EM_ERANGE = 0, 1, 2, 3, 4
+EM_OK, EM_EINVAL, EM_EDEVICE, EM_ENODEV, EM_ERANGE, EM_EIO = 0, 1, 2, 3, 4, 5
 KERNELS = {"automatic": 0, "naive": 1, "tiled": 2, "tiled_split": 3, "skinny": 4}
 STREAM_PER_THREAD = 2
 
@@ -34,6 +34,7 @@ EXPORTS = (
     "em_q8_register", "em_q8_unregister", "em_q8_registered",
     "em_attention_check", "em_attention_scratch_floats", "em_attention",
     "em_model_create", "em_model_destroy", "em_model_forward",
+    "em_model_load", "em_model_config_get", "em_model_read_weight",
 )
 ATTN_KERNELS = {"automatic": 0, "single_block": 1, "split": 2}
 
@@ -73,6 +74,10 @@ class DeviceError(EngineError, RuntimeError):
 
 class OutOfRange(EngineError, IndexError):
     """EM_ERANGE: the reference's std::out_of_range (check_feed)."""
+
+
+class CheckpointError(EngineError, RuntimeError):
+    """EM_EIO: the reference's std::runtime_error from load_checkpoint."""
 
 
 _sz = ctypes.c_size_t
@@ -138,6 +143,9 @@ def lib() -> ctypes.CDLL:
                                       ctypes.POINTER(_vp)]
         L.em_model_destroy.argtypes = [_vp]
         L.em_model_forward.argtypes = [_vp, _vp, _sz, _sz, _vp]
+        L.em_model_load.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(_vp)]
+        L.em_model_config_get.argtypes = [_vp, ctypes.POINTER(ModelConfig)]
+        L.em_model_read_weight.argtypes = [_vp, ctypes.c_char_p, _sz, _vp, _sz]
         for name in EXPORTS:
             getattr(L, name).restype = getattr(L, name).restype or ctypes.c_int
         _lib = L
@@ -152,6 +160,8 @@ def _check(rc: int) -> None:
         raise InvalidArgument(rc, msg)
     if rc == EM_ERANGE:
         raise OutOfRange(rc, msg)
+    if rc == EM_EIO:
+        raise CheckpointError(rc, msg)
     raise DeviceError(rc, msg)
 
 
@@ -375,9 +385,46 @@ class Model:
     wcls (dim x vocab) and `layers`, a list of dicts with rms_att, wqkv, wo,
     rms_ffn, w13, w2 (projections in x out)."""
 
+    @classmethod
+    def load(cls, path: str, q8: bool = False) -> "Model":
+        """em_model_load: a llama2.c v0 checkpoint straight onto the GPU."""
+        self = cls.__new__(cls)
+        handle = _vp()
+        _check(lib().em_model_load(os.fsencode(path), int(bool(q8)), ctypes.byref(handle)))
+        self.h = handle.value
+        cfg = ModelConfig()
+        _check(lib().em_model_config_get(self.h, ctypes.byref(cfg)))
+        self.config = {k: int(getattr(cfg, k)) for k, _ in ModelConfig._fields_}
+        self.q8 = bool(q8)
+        self._keep = []
+        return self
+
+    def weight(self, name: str, layer: int = 0):
+        """em_model_read_weight: the stored array (numpy), fp32, or int8 for an
+        int8 model's projections ("<name>.scale" for their scales)."""
+        import numpy as np
+        c = self.config
+        D, H, V = c["dim"], c["hidden_dim"], c["vocab_size"]
+        KV = c["n_kv_heads"] * (D // c["n_heads"])
+        shapes = {"token_embedding": (V, D), "rms_final": (D,), "wcls": (D, V), "rms_att": (D,),
+                  "rms_ffn": (D,), "wqkv": (D, D + 2 * KV), "wo": (D, D), "w13": (D, 2 * H),
+                  "w2": (H, D)}
+        base = name.split(".")[0]
+        shape = shapes[base]
+        if name.endswith(".scale"):
+            out = np.empty((shape[1],), np.float32)
+        elif self.q8 and base in ("wcls", "wqkv", "wo", "w13", "w2"):
+            out = np.empty(shape, np.int8)
+        else:
+            out = np.empty(shape, np.float32)
+        _check(lib().em_model_read_weight(self.h, name.encode(), layer, out.ctypes.data,
+                                          out.nbytes))
+        return out
+
     def __init__(self, config: dict, weights: dict, q8: bool = False):
         import numpy as np
         self.config = dict(config)
+        self.q8 = bool(q8)
         self._keep = []
 
         def host(a):

@@ -25,6 +25,8 @@
 // Everything runs on one stream the model owns, at default priority.
 #include <algorithm>
 #include <cmath>
+#include <cstdint>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <stdexcept>
@@ -117,6 +119,31 @@ __global__ __launch_bounds__(kThreads) void swiglu_kernel(int rows, int hidden, 
     }
 }
 
+// dst[i * ld + col0 + r] = src[r * in + i] for r < rows, i < in: a block
+// of `rows` rows of an (out x in) row-major matrix from a llama2.c file,
+// written transposed into columns col0 .. col0 + rows of the (in x ld)
+// destination (the CPU loader's read_transposed, model.cpp:43-53). 32 x 32
+// tiles through LDS (padded against bank conflicts): both the reads and the
+// writes are coalesced.
+__global__ __launch_bounds__(kThreads) void transpose_kernel(const float* __restrict__ src,
+                                                             std::size_t rows, std::size_t in,
+                                                             float* __restrict__ dst,
+                                                             std::size_t ld, std::size_t col0) {
+    __shared__ float tile[32][33];
+    const std::size_t r0 = static_cast<std::size_t>(blockIdx.y) * 32;
+    const std::size_t i0 = static_cast<std::size_t>(blockIdx.x) * 32;
+    const int tx = threadIdx.x % 32, ty = threadIdx.x / 32;
+    for (int k = ty; k < 32; k += kThreads / 32) {
+        const std::size_t r = r0 + k, i = i0 + tx;
+        if (r < rows && i < in) tile[k][tx] = src[r * in + i];
+    }
+    __syncthreads();
+    for (int k = ty; k < 32; k += kThreads / 32) {
+        const std::size_t i = i0 + k, r = r0 + tx;
+        if (r < rows && i < in) dst[i * ld + col0 + r] = tile[tx][k];
+    }
+}
+
 void check(hipError_t err, const char* what) { hip_check(err, what); }
 
 // Device buffer of T, freed with the owner.
@@ -194,10 +221,25 @@ struct LayerDev {
     Proj wqkv, wo, w13, w2;
 };
 
+// A llama2.c v0 checkpoint's header and size (model.cpp:61-90): the
+// reference's checks and messages.
+struct CheckpointInfo {
+    em_model_config cfg;
+    bool shared;
+};
+CheckpointInfo read_checkpoint_header(const std::string& path);
+
 class Model {
 public:
     Model(const em_model_config& c, const float* emb, const em_layer_weights* layers,
           const float* rms_final, const float* wcls, bool q8);
+    // Reads a llama2.c v0 checkpoint (load_checkpoint, model.cpp:115-163):
+    // the file streams through pinned memory to the GPU, which transposes
+    // and fuses the projections (q | k | v, gate | up) and quantises them.
+    Model(const std::string& path, const CheckpointInfo& info, bool q8);
+    const em_model_config& config() const { return cfg_; }
+    // The stored bytes of one weight array (see em_model_read_weight).
+    int read_weight(const std::string& name, std::size_t layer, void* dst, std::size_t bytes);
     ~Model();
     Model(const Model&) = delete;
     Model& operator=(const Model&) = delete;
@@ -206,6 +248,8 @@ public:
     int run(const int* tokens, std::size_t n, std::size_t pos, float* logits);
 
 private:
+    void init_runtime();
+    void quantize_proj(Proj& p);
     void upload(Buf<float>& b, const float* src, std::size_t count);
     void make_proj(Proj& p, const float* w, int rows, int cols, Buf<float>& staging);
     void project(int n, const float* in, const Proj& w, float* out, const float* rms,
@@ -273,10 +317,20 @@ Model::Model(const em_model_config& c, const float* emb, const em_layer_weights*
         make_proj(L.wo, w.wo, static_cast<int>(D), static_cast<int>(D), staging);
         make_proj(L.w13, w.w13, static_cast<int>(D), static_cast<int>(2 * H), staging);
         make_proj(L.w2, w.w2, static_cast<int>(H), static_cast<int>(D), staging);
+    }
+
+    init_runtime();
+}
+
+// Everything but the weights: caches, RoPE tables, feed and logits buffers.
+void Model::init_runtime() {
+    const em_model_config& c = cfg_;
+    const std::size_t D = c.dim, hs = c.dim / c.n_heads, V = c.vocab_size;
+    const std::size_t KV = c.n_kv_heads * hs;
+    for (LayerDev& L : layers_) {
         L.kcache.alloc(c.seq_len * KV);
         L.vcache.alloc(c.seq_len * KV);
     }
-
     // RoPE angles with the CPU model's float expressions (rope_tables,
     // model.cpp:179-192), so both models rotate by the same bits.
     const std::size_t half = hs / 2;
@@ -301,6 +355,272 @@ Model::Model(const em_model_config& c, const float* emb, const em_layer_weights*
     merge_kernel_ = mk && std::atoi(mk) != 0;
     check(hipStreamSynchronize(stream_), "load weights");
     reserve_rows(1);
+}
+
+// ---- llama2.c v0 checkpoint ---------------------------------------------
+
+// A checkpoint that cannot be opened or read, or whose header or size is
+// bad: EM_EIO (the reference's std::runtime_error from load_checkpoint).
+struct CheckpointError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+namespace {
+
+struct File {
+    FILE* f = nullptr;
+    explicit File(const std::string& path) : f(std::fopen(path.c_str(), "rb")) {}
+    ~File() {
+        if (f) std::fclose(f);
+    }
+};
+
+}  // namespace
+
+// parse_header and expected_size, model.cpp:61-90: every field non-zero and
+// all but the vocabulary positive (a positive vocabulary means the classifier
+// is the embedding); heads split evenly, even head size, whole kv groups; the
+// file exactly as long as the header implies.
+CheckpointInfo read_checkpoint_header(const std::string& path) {
+    File in(path);
+    if (!in.f) throw CheckpointError("cannot open checkpoint " + path);
+    std::fseek(in.f, 0, SEEK_END);
+    const std::uint64_t file_size = static_cast<std::uint64_t>(ftello(in.f));
+    std::fseek(in.f, 0, SEEK_SET);
+    std::int32_t h[7];
+    if (std::fread(h, sizeof(std::int32_t), 7, in.f) != 7)
+        throw CheckpointError("checkpoint " + path + " ended early");
+    CheckpointInfo info{};
+    info.shared = h[5] > 0;
+    for (int i = 0; i < 7; ++i)
+        if (h[i] == 0 || (i != 5 && h[i] < 0))
+            throw CheckpointError("checkpoint " + path + ": bad header field " + std::to_string(i) +
+                                  " = " + std::to_string(h[i]));
+    auto u = [](std::int32_t v) { return static_cast<std::size_t>(v < 0 ? -std::int64_t{v} : v); };
+    em_model_config& c = info.cfg;
+    c = {u(h[0]), u(h[1]), u(h[2]), u(h[3]), u(h[4]), u(h[5]), u(h[6])};
+    if (c.dim % c.n_heads != 0 || (c.dim / c.n_heads) % 2 != 0 || c.n_heads % c.n_kv_heads != 0)
+        throw CheckpointError("checkpoint " + path +
+                              ": dim must split into even-sized heads, and query heads into whole "
+                              "groups per kv head");
+    const std::uint64_t D = c.dim, H = c.hidden_dim, hs = c.dim / c.n_heads;
+    const std::uint64_t KV = c.n_kv_heads * hs, V = c.vocab_size;
+    const std::uint64_t per_layer = 2 * D + 2 * D * D + 2 * D * KV + 3 * D * H;
+    std::uint64_t floats = V * D + c.n_layers * per_layer + D + std::uint64_t{c.seq_len} * hs;
+    if (!info.shared) floats += V * D;
+    const std::uint64_t want = 7 * sizeof(std::int32_t) + floats * sizeof(float);
+    if (file_size != want)
+        throw CheckpointError("checkpoint " + path + " is " + std::to_string(file_size) +
+                              " bytes, header implies " + std::to_string(want));
+    return info;
+}
+
+namespace {
+
+// Streams a checkpoint's float sections to the GPU: two pinned chunks and
+// two device staging chunks in turn, so reading one chunk from the file
+// overlaps the copy and transpose of the previous one.
+class Streamer {
+public:
+    static constexpr std::size_t kChunk = 64u << 20;  // bytes
+
+    Streamer(const std::string& path, hipStream_t s) : path_(path), in_(path), s_(s) {
+        if (!in_.f) throw CheckpointError("cannot open checkpoint " + path);
+        std::fseek(in_.f, 7 * sizeof(std::int32_t), SEEK_SET);
+        for (int b = 0; b < 2; ++b) {
+            check(hipHostMalloc(&host_[b], kChunk, hipHostMallocDefault), "pinned staging");
+            check(hipMalloc(&dev_[b], kChunk), "device staging");
+            check(hipEventCreateWithFlags(&done_[b], hipEventDisableTiming), "event");
+        }
+    }
+    ~Streamer() {
+        (void)hipStreamSynchronize(s_);
+        for (int b = 0; b < 2; ++b) {
+            if (done_[b]) (void)hipEventDestroy(done_[b]);
+            if (dev_[b]) (void)hipFree(dev_[b]);
+            if (host_[b]) (void)hipHostFree(host_[b]);
+        }
+    }
+    Streamer(const Streamer&) = delete;
+    Streamer& operator=(const Streamer&) = delete;
+
+    // `count` floats straight into dst.
+    void plain(float* dst, std::size_t count) {
+        const std::size_t per = kChunk / sizeof(float);
+        for (std::size_t done = 0; done < count; done += per) {
+            const std::size_t n = std::min(per, count - done);
+            float* h = next(n);
+            check(hipMemcpyAsync(dst + done, h, n * sizeof(float), hipMemcpyHostToDevice, s_),
+                  "upload checkpoint");
+            check(hipEventRecord(done_[cur_], s_), "event");
+        }
+    }
+
+    // An (out x in) row-major matrix, transposed into columns col0 .. col0 +
+    // out of dst (in x ld): read_transposed, model.cpp:43-53.
+    void transposed(std::size_t out, std::size_t in, float* dst, std::size_t ld, std::size_t col0) {
+        const std::size_t rows_per = std::max<std::size_t>(1, kChunk / sizeof(float) / in);
+        for (std::size_t r = 0; r < out; r += rows_per) {
+            const std::size_t rows = std::min(rows_per, out - r);
+            float* h = next(rows * in);
+            float* d = dev_[cur_];
+            check(hipMemcpyAsync(d, h, rows * in * sizeof(float), hipMemcpyHostToDevice, s_),
+                  "upload checkpoint");
+            const dim3 grid(ceil_div(static_cast<long long>(in), 32),
+                            ceil_div(static_cast<long long>(rows), 32));
+            hipLaunchKernelGGL(transpose_kernel, grid, dim3(kThreads), 0, s_, d, rows, in, dst, ld,
+                               col0 + r);
+            check(hipGetLastError(), "launch");
+            check(hipEventRecord(done_[cur_], s_), "event");
+        }
+    }
+
+    void skip_floats(std::size_t n) {
+        if (std::fseek(in_.f, static_cast<long>(n * sizeof(float)), SEEK_CUR) != 0)
+            throw CheckpointError("checkpoint " + path_ + " ended early");
+    }
+
+private:
+    // The next pinned chunk, filled with n floats from the file, once the
+    // work that last used it (and its device twin) has finished.
+    float* next(std::size_t n) {
+        cur_ ^= 1;
+        check(hipEventSynchronize(done_[cur_]), "staging reuse");
+        float* h = static_cast<float*>(host_[cur_]);
+        if (std::fread(h, sizeof(float), n, in_.f) != n)
+            throw CheckpointError("checkpoint " + path_ + " ended early");
+        return h;
+    }
+
+    std::string path_;
+    File in_;
+    hipStream_t s_;
+    void* host_[2] = {};
+    float* dev_[2] = {};
+    hipEvent_t done_[2] = {};
+    int cur_ = 1;
+};
+
+}  // namespace
+
+// load_checkpoint's order (model.cpp:133-162): the file groups each weight
+// across all layers (every layer's wq, then every wk, ...); projections are
+// stored out x in and land transposed, q | k | v into wqkv and w1 | w3 into
+// w13. The RoPE tables at the end are skipped (recomputed); a positive
+// vocabulary makes the classifier the embedding's transpose. With q8 each
+// projection is then quantised on the GPU (quantize_q8, bit-exact).
+Model::Model(const std::string& path, const CheckpointInfo& info, bool q8)
+    : cfg_(info.cfg), q8_(q8), feed_host_(info.cfg.seq_len + 1),
+      logits_host_(info.cfg.vocab_size) {
+    const em_model_config& c = cfg_;
+    const std::size_t D = c.dim, H = c.hidden_dim, hs = c.dim / c.n_heads;
+    const std::size_t KV = c.n_kv_heads * hs, V = c.vocab_size, QKV = D + 2 * KV;
+    shape_ = {static_cast<int>(c.n_heads), static_cast<int>(c.n_kv_heads), static_cast<int>(hs),
+              static_cast<int>(c.seq_len), QKV, KV, D};
+    layers_ = std::vector<LayerDev>(c.n_layers);
+    auto fp32 = [&](Proj& p, std::size_t rows, std::size_t cols) {
+        p.rows = static_cast<int>(rows);
+        p.cols = static_cast<int>(cols);
+        p.f32.alloc(rows * cols);
+    };
+    emb_.alloc(V * D);
+    rms_final_.alloc(D);
+    fp32(wcls_, D, V);
+    for (LayerDev& L : layers_) {
+        L.rms_att.alloc(D);
+        L.rms_ffn.alloc(D);
+        fp32(L.wqkv, D, QKV);
+        fp32(L.wo, D, D);
+        fp32(L.w13, D, 2 * H);
+        fp32(L.w2, H, D);
+    }
+    {
+        Streamer r(path, stream_);
+        r.plain(emb_.p, V * D);
+        for (LayerDev& L : layers_) r.plain(L.rms_att.p, D);
+        for (LayerDev& L : layers_) r.transposed(D, D, L.wqkv.f32.p, QKV, 0);
+        for (LayerDev& L : layers_) r.transposed(KV, D, L.wqkv.f32.p, QKV, D);
+        for (LayerDev& L : layers_) r.transposed(KV, D, L.wqkv.f32.p, QKV, D + KV);
+        for (LayerDev& L : layers_) r.transposed(D, D, L.wo.f32.p, D, 0);
+        for (LayerDev& L : layers_) r.plain(L.rms_ffn.p, D);
+        for (LayerDev& L : layers_) r.transposed(H, D, L.w13.f32.p, 2 * H, 0);
+        for (LayerDev& L : layers_) r.transposed(D, H, L.w2.f32.p, D, 0);
+        for (LayerDev& L : layers_) r.transposed(H, D, L.w13.f32.p, 2 * H, H);
+        r.plain(rms_final_.p, D);
+        r.skip_floats(c.seq_len * hs);
+        if (info.shared) {
+            const dim3 grid(ceil_div(static_cast<long long>(D), 32),
+                            ceil_div(static_cast<long long>(V), 32));
+            hipLaunchKernelGGL(transpose_kernel, grid, dim3(kThreads), 0, stream_, emb_.p, V, D,
+                               wcls_.f32.p, V, std::size_t{0});
+            check(hipGetLastError(), "launch");
+        } else {
+            r.transposed(V, D, wcls_.f32.p, V, 0);
+        }
+        check(hipStreamSynchronize(stream_), "load checkpoint");
+    }
+    if (q8_) {
+        quantize_proj(wcls_);
+        for (LayerDev& L : layers_) {
+            quantize_proj(L.wqkv);
+            quantize_proj(L.wo);
+            quantize_proj(L.w13);
+            quantize_proj(L.w2);
+        }
+    }
+    init_runtime();
+}
+
+// fp32 weights already on the device -> int8 + scales (quantize_q8), the
+// fp32 copy freed once the stream has used it.
+void Model::quantize_proj(Proj& p) {
+    p.q8.alloc(static_cast<std::size_t>(p.rows) * p.cols);
+    p.scale.alloc(p.cols);
+    run_quantize_q8(p.rows, p.cols, p.f32.p, p.q8.p, p.scale.p, stream_);
+    check(hipGetLastError(), "launch");
+    check(hipStreamSynchronize(stream_), "quantize weights");
+    p.f32.alloc(0);
+}
+
+// The array named like ref_ckpt_array / LayerWeights (model.h:29-43): fp32
+// arrays as floats; an int8 model's projections as their int8 bytes, and
+// "<name>.scale" as their column scales. bytes must be the array's size.
+int Model::read_weight(const std::string& name, std::size_t layer, void* dst, std::size_t bytes) {
+    const void* src = nullptr;
+    std::size_t size = 0;
+    auto from = [&](const void* p, std::size_t n) {
+        src = p;
+        size = n;
+    };
+    auto proj = [&](const Proj& w, const std::string& base) {
+        const std::size_t count = static_cast<std::size_t>(w.rows) * w.cols;
+        if (name == base) {
+            if (q8_) from(w.q8.p, count);
+            else from(w.f32.p, count * sizeof(float));
+        } else if (q8_ && name == base + ".scale") {
+            from(w.scale.p, w.cols * sizeof(float));
+        }
+    };
+    const std::size_t D = cfg_.dim, V = cfg_.vocab_size;
+    if (name == "token_embedding") from(emb_.p, V * D * sizeof(float));
+    else if (name == "rms_final") from(rms_final_.p, D * sizeof(float));
+    else if (name.rfind("wcls", 0) == 0) proj(wcls_, "wcls");
+    else if (layer < layers_.size()) {
+        const LayerDev& L = layers_[layer];
+        if (name == "rms_att") from(L.rms_att.p, D * sizeof(float));
+        else if (name == "rms_ffn") from(L.rms_ffn.p, D * sizeof(float));
+        else if (name.rfind("wqkv", 0) == 0) proj(L.wqkv, "wqkv");
+        else if (name.rfind("wo", 0) == 0) proj(L.wo, "wo");
+        else if (name.rfind("w13", 0) == 0) proj(L.w13, "w13");
+        else if (name.rfind("w2", 0) == 0) proj(L.w2, "w2");
+    }
+    if (!src) return fail(EM_EINVAL, "read_weight: no array " + name + " in layer " + std::to_string(layer));
+    if (bytes != size)
+        return fail(EM_EINVAL, "read_weight: " + name + " is " + std::to_string(size) +
+                                   " bytes, not " + std::to_string(bytes));
+    check(hipMemcpyAsync(dst, src, size, hipMemcpyDeviceToHost, stream_), "read weight");
+    check(hipStreamSynchronize(stream_), "read weight");
+    return EM_OK;
 }
 
 Model::~Model() { (void)hipStreamSynchronize(stream_); }
@@ -580,6 +900,8 @@ struct em_model {
     em_model(const em_model_config& c, const float* emb, const em_layer_weights* layers,
              const float* rms_final, const float* wcls, bool q8)
         : impl(c, emb, layers, rms_final, wcls, q8) {}
+    em_model(const std::string& path, const em::CheckpointInfo& info, bool q8)
+        : impl(path, info, q8) {}
 };
 
 using em::fail;
@@ -589,6 +911,26 @@ namespace {
 bool too_big(std::size_t a, std::size_t b) {
     constexpr std::size_t kLimit = (std::size_t{1} << 31) - 1;
     return a != 0 && b > kLimit / a;
+}
+
+// EM_OK if the forward pass can run config c (sizes, 32-bit indexing, a
+// shape the attention kernels take), else EM_EINVAL with the reason.
+int check_config(const em_model_config& c) {
+    if (!c.dim || !c.hidden_dim || !c.n_layers || !c.n_heads || !c.n_kv_heads || !c.vocab_size ||
+        !c.seq_len || c.dim % c.n_heads)
+        return fail(EM_EINVAL, "CudaTransformer: bad config");
+    const std::size_t hs = c.dim / c.n_heads, KV = c.n_kv_heads * hs;
+    if (c.dim > (1u << 30) || c.seq_len > (1u << 30) || too_big(c.vocab_size, c.dim) ||
+        too_big(c.dim, c.dim + 2 * KV) || too_big(c.dim, 2 * c.hidden_dim) ||
+        too_big(c.seq_len, KV) || too_big(c.seq_len + 8, c.dim + 2 * KV) ||
+        too_big(c.seq_len, 2 * c.hidden_dim))
+        return fail(EM_EINVAL, "CudaTransformer: more than 2^31 elements");
+    const em::AttnShape shape{static_cast<int>(c.n_heads), static_cast<int>(c.n_kv_heads),
+                              static_cast<int>(hs), static_cast<int>(c.seq_len),
+                              c.dim + 2 * KV, KV, c.dim};
+    const std::string why = em::attention_reject(shape, em::kAttnAutomatic);
+    if (!why.empty()) return fail(EM_EINVAL, "CudaTransformer: " + why);
+    return EM_OK;
 }
 
 }  // namespace
@@ -604,20 +946,7 @@ int em_model_create(const em_model_config* cfg, const float* token_embedding,
     const em_model_config& c = *cfg;
     if (weight_type != EM_WEIGHTS_F32 && weight_type != EM_WEIGHTS_Q8)
         return fail(EM_EINVAL, "CudaTransformer: unknown weight type");
-    if (!c.dim || !c.hidden_dim || !c.n_layers || !c.n_heads || !c.n_kv_heads || !c.vocab_size ||
-        !c.seq_len || c.dim % c.n_heads)
-        return fail(EM_EINVAL, "CudaTransformer: bad config");
-    const std::size_t hs = c.dim / c.n_heads, KV = c.n_kv_heads * hs;
-    if (c.dim > (1u << 30) || c.seq_len > (1u << 30) || too_big(c.vocab_size, c.dim) ||
-        too_big(c.dim, c.dim + 2 * KV) || too_big(c.dim, 2 * c.hidden_dim) ||
-        too_big(c.seq_len, KV) || too_big(c.seq_len + 8, c.dim + 2 * KV) ||
-        too_big(c.seq_len, 2 * c.hidden_dim))
-        return fail(EM_EINVAL, "CudaTransformer: more than 2^31 elements");
-    const em::AttnShape shape{static_cast<int>(c.n_heads), static_cast<int>(c.n_kv_heads),
-                              static_cast<int>(hs), static_cast<int>(c.seq_len),
-                              c.dim + 2 * KV, KV, c.dim};
-    const std::string why = em::attention_reject(shape, em::kAttnAutomatic);
-    if (!why.empty()) return fail(EM_EINVAL, "CudaTransformer: " + why);
+    if (const int rc = check_config(c)) return rc;
     if (!token_embedding || !layers || !rms_final || !wcls)
         return fail(EM_EINVAL, "CudaTransformer: null weights");
     for (std::size_t l = 0; l < c.n_layers; ++l) {
@@ -633,6 +962,45 @@ int em_model_create(const em_model_config* cfg, const float* token_embedding,
         return fail(EM_EDEVICE, std::string("CudaTransformer: ") + e.what());
     }
     return EM_OK;
+}
+
+int em_model_load(const char* path, int weight_type, em_model** out) {
+    if (!out) return fail(EM_EINVAL, "load_checkpoint: null output pointer");
+    *out = nullptr;
+    if (!path) return fail(EM_EINVAL, "load_checkpoint: null path");
+    if (weight_type != EM_WEIGHTS_F32 && weight_type != EM_WEIGHTS_Q8)
+        return fail(EM_EINVAL, "CudaTransformer: unknown weight type");
+    em::CheckpointInfo info{};
+    try {
+        info = em::read_checkpoint_header(path);
+    } catch (const std::exception& e) {
+        return fail(EM_EIO, e.what());
+    }
+    if (const int rc = check_config(info.cfg)) return rc;
+    if (!em::device_present()) return fail(EM_ENODEV, "CudaTransformer: no usable GPU");
+    try {
+        *out = new em_model(path, info, weight_type == EM_WEIGHTS_Q8);
+    } catch (const em::CheckpointError& e) {
+        return fail(EM_EIO, e.what());
+    } catch (const std::exception& e) {
+        return fail(EM_EDEVICE, std::string("CudaTransformer: ") + e.what());
+    }
+    return EM_OK;
+}
+
+int em_model_config_get(const em_model* m, em_model_config* out) {
+    if (!m || !out) return fail(EM_EINVAL, "config: null pointer");
+    *out = m->impl.config();
+    return EM_OK;
+}
+
+int em_model_read_weight(em_model* m, const char* name, size_t layer, void* dst, size_t bytes) {
+    if (!m || !name || !dst) return fail(EM_EINVAL, "read_weight: null pointer");
+    try {
+        return m->impl.read_weight(name, layer, dst, bytes);
+    } catch (const std::exception& e) {
+        return fail(EM_EDEVICE, e.what());
+    }
 }
 
 int em_model_destroy(em_model* m) {
