@@ -375,6 +375,51 @@ def llama7b_case(em, torch, steps):
     return out
 
 
+def checkpoint_load_case(em, torch) -> dict:
+    """Loading a llama2.c v0 checkpoint with em_model_load: the file streamed
+    to the GPU through pinned chunks, projections transposed, fused and (q8)
+    quantised there (the reference reads it with load_checkpoint on the host,
+    model.cpp:115-163). Files: stories15M's shape and a one-layer Llama-7B
+    shape (dim 4096, hidden 11008, vocab 32000, tied classifier, 1.33 GB),
+    random ~N(0, 0.02), written to a temporary directory first (not timed).
+    Wall-clock seconds, best of 2, the file in the page cache."""
+    import tempfile
+    import numpy as np
+    out = {}
+    rng = np.random.default_rng(11)
+    shapes = {"stories15M": (288, 768, 6, 6, 6, 32000, 256),
+              "llama7b_1layer": (4096, 11008, 1, 32, 32, 32000, 512)}
+    with tempfile.TemporaryDirectory() as tmp:
+        for name, (D, H, L, nh, nkv, V, S) in shapes.items():
+            path = os.path.join(tmp, name + ".bin")
+            KV = nkv * (D // nh)
+            with open(path, "wb") as f:
+                f.write(np.array([D, H, L, nh, nkv, V, S], np.int32).tobytes())
+                for count in (V * D, L * D, L * D * D, L * KV * D, L * KV * D, L * D * D, L * D,
+                              L * H * D, L * D * H, L * H * D, D, S * (D // nh)):
+                    left = count
+                    while left:
+                        n = min(left, 1 << 26)
+                        f.write((rng.standard_normal(n, dtype=np.float32) * 0.02).tobytes())
+                        left -= n
+            size = os.path.getsize(path)
+            row = {"file_MB": round(size / 1e6, 1)}
+            for q8 in (False, True):
+                best = None
+                for _ in range(2):
+                    t0 = time.perf_counter()
+                    m = em.Model.load(path, q8=q8)
+                    best = min(best or 1e9, time.perf_counter() - t0)
+                    m.close()
+                tag = "q8" if q8 else "f32"
+                row[f"em_model_load_{tag}_s"] = round(best, 3)
+                row[f"em_model_load_{tag}_GBps"] = round(size / best / 1e9, 2)
+            out[name] = row
+            os.remove(path)
+    out["note"] = "wall-clock s, best of 2, file in the page cache after the first read"
+    return out
+
+
 def host_median_convention(em, torch, A, w, s, C, reps=101):
     """The reference's bench_cuda convention: host time launch -> synchronize."""
     em.matmul(A, w, C, scale=s)
@@ -971,6 +1016,8 @@ def main() -> int:
         progress("attention done")
         extra["stories15m_forward"] = stories15m_case(em, torch)
         progress("stories15M done")
+        extra["checkpoint_load"] = checkpoint_load_case(em, torch)
+        progress("checkpoint load done")
         extra["llama7b_model_2layers_int8"] = llama7b_model_case(em, torch)
         extra["llama7b_model_2layers_int8_gqa8"] = llama7b_model_case(em, torch, n_kv_heads=8)
         progress("llama7b models done")

@@ -164,15 +164,85 @@ def test_split_k_queue_is_deterministic():
                     f"case {i // 3}: repeat differs"
 
 
-def test_reuse_and_scratch_generation():
+def test_reuse_across_growing_scratch():
     # test_cuda.cpp:93-105: shapes of growing split-K scratch, one after another.
-    gen0 = em.scratch_generation()
     for i, (m, k, n) in enumerate([(1, 2000, 300), (4, 100, 5000), (64, 3000, 64), (200, 64, 64),
                                    (2, 8192, 8192)]):
         A, B = seeded(m, k, n, 5 + 2 * i)
         got = host(em.matmul(dev(A), dev(B)))
         check(got, orc.matmul_naive(A, B), A, B, k)
-    assert em.scratch_generation() >= gen0
+
+
+def big_skinny(seed, k=65536):
+    """An int8 skinny product whose split-K partials (8 rows x 16384 columns
+    x k / 256 slices: 128 MiB at k = 65536) outgrow every other test's;
+    B stays under the 2^31 elements the entry points accept."""
+    m, n = 8, 16384
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    B = torch.randint(-127, 128, (k, n), generator=g, device="cuda", dtype=torch.int8)
+    s = torch.rand((n,), generator=g, device="cuda") * 1e-3
+    A = torch.randn((m, k), generator=g, device="cuda")
+    return A, B, s
+
+
+def test_scratch_generation_bumps_on_growth_only():
+    # cuda_scratch_generation (src/cuda_matmul.h:112, cuda_matmul.cu:268-281,567):
+    # growing the scratch bumps it; a shape that fits what is there does not.
+    A, B, s = big_skinny(1)
+    gen0 = em.scratch_generation()
+    C1 = em.matmul(A, B, scale=s, kernel="skinny")
+    torch.cuda.synchronize()
+    gen1 = em.scratch_generation()
+    assert gen1 > gen0
+    C2 = em.matmul(A, B, scale=s, kernel="skinny")
+    torch.cuda.synchronize()
+    assert em.scratch_generation() == gen1  # same shape: no growth
+    assert torch.equal(C1, C2)
+    A2, B2 = seeded(4, 3000, 2000, 17)
+    got = host(em.matmul(dev(A2), dev(B2), kernel="skinny"))  # smaller: fits
+    assert em.scratch_generation() == gen1
+    check(got, orc.matmul_naive(A2, B2), A2, B2, 3000)
+    del A, B, s, C1, C2
+    torch.cuda.synchronize()
+
+
+def test_graph_recaptured_after_generation_bump():
+    # The graph user's rule (cuda_model.cu:175-177,196): a graph captured
+    # before a bump points at freed scratch, so it is captured again; the new
+    # graph's replays equal eager results. (The old graph is not replayed.)
+    m, k, n = 2, 8192, 4096
+    A, B = seeded(m, k, n, 23)
+    dA, dB = dev(A), dev(B)
+    C = torch.empty((m, n), device="cuda")
+
+    def capture():
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            em.matmul(dA, dB, C, kernel="skinny")
+        return g
+
+    em.matmul(dA, dB, C, kernel="skinny")  # scratch for this shape exists
+    eager = host(C).copy()
+    g = capture()
+    gen = em.scratch_generation()
+    g.replay()
+    assert np.array_equal(host(C), eager)
+    Ab, Bb, sb = big_skinny(2, k=98304)  # 384 slices: past the generation test's 256
+    em.matmul(Ab, Bb, scale=sb, kernel="skinny")  # grows the scratch
+    torch.cuda.synchronize()
+    assert em.scratch_generation() > gen
+    del g, Ab, Bb, sb
+    g = capture()
+    for _ in range(3):
+        C.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        assert np.array_equal(host(C), eager)
+    del g
+    torch.cuda.synchronize()
 
 
 def test_bad_shapes_on_device():
