@@ -286,6 +286,10 @@ private:
     // EM_DECODE_MERGE_KERNEL=1 at creation: one-row steps merge the
     // attention chunks with the merge kernel, not in the wo GEMV (tests).
     bool merge_kernel_ = false;
+    // EM_PREFILL_ROPE_FUSION=0 at creation: the exact-split qkv product of
+    // prefill rows writes qkv_ and rope_cache_kernel follows, rather than
+    // RoPE and the cache write in the product's epilogue (tests).
+    bool rope_fusion_ = true;
     Buf<float> ssq_;
 
     Pinned<int> feed_host_;  // [pos, tokens...]
@@ -353,6 +357,8 @@ void Model::init_runtime() {
     if (use_ssq_) ssq_.alloc(D / kSsqChunk);
     const char* mk = std::getenv("EM_DECODE_MERGE_KERNEL");
     merge_kernel_ = mk && std::atoi(mk) != 0;
+    const char* rf = std::getenv("EM_PREFILL_ROPE_FUSION");
+    rope_fusion_ = !rf || std::atoi(rf) != 0;
     check(hipStreamSynchronize(stream_), "load weights");
     reserve_rows(1);
 }
@@ -729,7 +735,7 @@ bool Model::qkv_exact_split(int n, LayerDev& L, bool* roped) {
     const RopeFuse r{feed_dev_.p, rope_cos_.p, rope_sin_.p, L.kcache.p, L.vcache.p,
                      static_cast<int>(cfg_.dim), static_cast<int>(shape_.kv_stride),
                      shape_.head_size};
-    *roped = run_split_bf16(a, &r);
+    *roped = run_split_bf16(a, rope_fusion_ ? &r : nullptr);
     check(hipGetLastError(), "launch");
     return true;
 }

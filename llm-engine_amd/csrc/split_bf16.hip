@@ -12,7 +12,28 @@
 // and v_mfma_f32_16x16x32_bf16 sums them into fp32 accumulators. Nothing is
 // dropped: the result differs from an fp32 FMA chain only in summation order,
 // as any reordered fp32 sum does, and the column scale is applied to the
-// finished sum as in the GEMV path. At 16 cycles per 8192 multiply-adds
+// finished sum as in the GEMV path.
+//
+// Range. gfx950's bf16 MFMA keeps subnormal operands, products and sums
+// (checked on the device), so the split stays exact while every term is a
+// bf16 value: down to |a| = 2^-110 (the lo term's last bit at 2^-133,
+// bf16's smallest subnormal). Smaller values (fp32 subnormals, or rows near
+// 1e-37) would lose low bits. The pre-pass, which holds each row, scales it
+// by 2^s, s = max(0, 64 - e) for its largest finite magnitude 2^e, and the
+// kernel scales each sum of the row back by 2^-s (after the column scale
+// when it writes C): both exact in fp32 short of a subnormal result, which
+// rounds once, so a row that needs no scaling gets the same bits either way.
+// The kernel that splits A itself runs unscaled, ORs its lo remainders
+// (their low half is non-zero iff bits were dropped) and checks its sums;
+// a 16-row block with dropped bits or a non-finite sum is computed again by
+// fp32 multiply-adds (fma_block), whose products of such values keep their
+// relative precision. An infinite activation passes through the pre-pass as
+// hi = a, mid = lo = 0 (and through fma_block as itself), so C gets +-inf,
+// NaN where its weight is 0, as fp32 arithmetic gives; a NaN gives NaN. The
+// products sum a * q before the column scale, as the GEMV does, so
+// |a| * 127 * k past fp32's range overflows where a * (q * scale) might not.
+//
+// Speed. At 16 cycles per 8192 multiply-adds
 // the three terms cost 3/16 of fp32 MFMA time (16x16x4 f32: 32 cycles per
 // 1024); measured against the fp32-MFMA tiled_split kernel at 4096^2 it is
 // 1.1x faster at m = 9-16, 1.9x at m = 64 and 2.6x at m = 512. VALU work
@@ -57,30 +78,80 @@ constexpr int kTileStride = kTile + 4;   // LDS row stride of the epilogue tile
 __device__ __forceinline__ uint32_t bits(float f) { return __builtin_bit_cast(uint32_t, f); }
 __device__ __forceinline__ float from_bits(uint32_t u) { return __builtin_bit_cast(float, u); }
 
-// a = hi + mid + lo exactly; each part's bits are the top half of an fp32.
+// a = hi + mid + lo exactly for |a| >= 2^-110; each part's bits are the top
+// half of an fp32. +-inf: hi = a, mid = lo = 0 (a - hi would be NaN).
 __device__ __forceinline__ void split3(float a, uint32_t& hi, uint32_t& mid, uint32_t& lo) {
 #pragma clang fp contract(off)
     hi = bits(a) >> 16;
-    const float r1 = a - from_bits(hi << 16);
+    const float h = from_bits(hi << 16);
+    const float r1 = a == h ? 0.0f : a - h;
     mid = bits(r1) >> 16;
     const float r2 = r1 - from_bits(mid << 16);
     lo = bits(r2) >> 16;
 }
 
+// The row scale's exponent: the largest finite magnitude is brought to
+// [2^64, 2^65) when it lies below (values down to 2^-174 of it then split
+// exactly, and a sum of k < 2^31 scaled products stays below 2^103).
+constexpr int kShiftTarget = 64;
+
+__device__ __forceinline__ float finite_mag(float x) {
+    const float m = fabsf(x);
+    return m < __builtin_inff() ? m : 0.0f;  // NaN and inf count as 0
+}
+
+__device__ __forceinline__ int row_shift(float max_mag) {
+    const uint32_t u = bits(max_mag);
+    if (u == 0) return 0;
+    const int e = u >= 0x00800000u ? static_cast<int>(u >> 23) - 127 : 31 - __clz(u) - 149;
+    return max(0, kShiftTarget - e);
+}
+
+// block_sum(ss) and block_max(mx) over one pair of barriers (the sum in
+// block_sum's order). `part` is 8 floats of LDS.
+__device__ __forceinline__ void block_sum_max(float& ss, float& mx, float* part) {
+    ss = wave_sum(ss);
+    mx = wave_max(mx);
+    const int wave = threadIdx.x / kWave;
+    __syncthreads();
+    if ((threadIdx.x % kWave) == 0) {
+        part[wave] = ss;
+        part[4 + wave] = mx;
+    }
+    __syncthreads();
+    ss = (part[0] + part[1]) + (part[2] + part[3]);
+    mx = fmaxf(fmaxf(part[4], part[5]), fmaxf(part[6], part[7]));
+}
+
 // Row r of A3 (three planes, m_pad x k_pad each): rmsnorm(A[r]) * w when w is
-// given (the arithmetic of rmsnorm_rows: x * s * w[j]), zeros past m and k.
+// given (the arithmetic of rmsnorm_rows: x * s * w[j]), times 2^shifts[r];
+// zeros past m and k. The shift comes from the row's largest finite |x|, or
+// with the norm from s * max |x * w[j]| (within rounding of the normed
+// row's largest, found in the sum of squares' pass).
 __global__ __launch_bounds__(kThreads) void split_a_kernel(int m, int k, int m_pad, int k_pad,
                                                            const float* A, const float* w,
-                                                           uint16_t* A3) {
-    __shared__ float part[4];
+                                                           uint16_t* A3, int* shifts) {
+    __shared__ float part[8];
     const int r = blockIdx.x;
     const float* in = A + static_cast<std::size_t>(r) * k;
-    float s = 1.0f;
-    if (w && r < m) {
-        float ss = 0.0f;
-        for (int j = threadIdx.x; j < k; j += kThreads) ss = fmaf(in[j], in[j], ss);
-        s = 1.0f / sqrtf(block_sum(ss, part) / static_cast<float>(k) + kRmsEps);
+    float s = 1.0f, top = 0.0f;
+    if (r < m) {
+        float ss = 0.0f, mx = 0.0f;
+        if (w) {
+            for (int j = threadIdx.x; j < k; j += kThreads) {
+                ss = fmaf(in[j], in[j], ss);
+                mx = fmaxf(mx, finite_mag(in[j] * w[j]));
+            }
+            block_sum_max(ss, mx, part);
+            s = 1.0f / sqrtf(ss / static_cast<float>(k) + kRmsEps);
+            top = s * mx;
+        } else {
+            for (int j = threadIdx.x; j < k; j += kThreads) mx = fmaxf(mx, finite_mag(in[j]));
+            top = block_max(mx, part);
+        }
     }
+    const int shift = row_shift(top);
+    if (threadIdx.x == 0) shifts[r] = shift;
     const std::size_t plane = static_cast<std::size_t>(m_pad) * k_pad;
     uint16_t* o = A3 + static_cast<std::size_t>(r) * k_pad;
     // Eight k per thread per step: one 16-byte store per plane.
@@ -91,7 +162,7 @@ __global__ __launch_bounds__(kThreads) void split_a_kernel(int m, int k, int m_p
             const int j = j0 + e;
             float a = 0.0f;
             if (r < m && j < k) a = w ? in[j] * s * w[j] : in[j];
-            split3(a, h[e], md[e], l[e]);
+            split3(__builtin_ldexpf(a, shift), h[e], md[e], l[e]);
         }
         auto pack = [](const uint32_t* v) {
             return make_uint4(v[0] | v[1] << 16, v[2] | v[3] << 16, v[4] | v[5] << 16,
@@ -114,8 +185,9 @@ __global__ __launch_bounds__(kThreads) void split_a_row_kernel(int m, int k, int
                                                                int vec4,
                                                                const float* __restrict__ A,
                                                                const float* __restrict__ w,
-                                                               uint16_t* __restrict__ A3) {
-    __shared__ float part[4];
+                                                               uint16_t* __restrict__ A3,
+                                                               int* __restrict__ shifts) {
+    __shared__ float part[8];
     const int r = blockIdx.x;
     const bool live = r < m;  // rows past m are zeros
     const float* in = A + static_cast<std::size_t>(live ? r : 0) * k;
@@ -139,15 +211,32 @@ __global__ __launch_bounds__(kThreads) void split_a_row_kernel(int m, int k, int
             for (int e = 0; e < 8; ++e) wv[st][e] = j0 + e < k ? w[j0 + e] : 1.0f;
         }
     }
-    float s = 1.0f;
-    if (w && live) {
-        float ss = 0.0f;
+    // The norm and the shift, as split_a_kernel finds them, with one
+    // reduction (values past k are 0, weights there 1).
+    float s = 1.0f, top = 0.0f;
+    if (live) {
+        float ss = 0.0f, mx = 0.0f;
 #pragma unroll
         for (int st = 0; st < S; ++st)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) ss = fmaf(v[st][e], v[st][e], ss);
-        s = 1.0f / sqrtf(block_sum(ss, part) / static_cast<float>(k) + kRmsEps);
+            for (int e = 0; e < 8; ++e) {
+                if (w) {
+                    ss = fmaf(v[st][e], v[st][e], ss);
+                    mx = fmaxf(mx, finite_mag(v[st][e] * wv[st][e]));
+                } else {
+                    mx = fmaxf(mx, finite_mag(v[st][e]));
+                }
+            }
+        if (w) {
+            block_sum_max(ss, mx, part);
+            s = 1.0f / sqrtf(ss / static_cast<float>(k) + kRmsEps);
+            top = s * mx;
+        } else {
+            top = block_max(mx, part);
+        }
     }
+    const int shift = row_shift(top);
+    if (threadIdx.x == 0) shifts[r] = shift;
     const std::size_t plane = static_cast<std::size_t>(m_pad) * k_pad;
     uint16_t* o = A3 + static_cast<std::size_t>(r) * k_pad;
 #pragma unroll
@@ -159,7 +248,7 @@ __global__ __launch_bounds__(kThreads) void split_a_row_kernel(int m, int k, int
         for (int e = 0; e < 8; ++e) {
             const int j = j0 + e;
             const float a = w && j < k ? v[st][e] * s * wv[st][e] : v[st][e];
-            split3(a, h[e], md[e], l[e]);
+            split3(__builtin_ldexpf(a, shift), h[e], md[e], l[e]);
         }
         auto pack = [](const uint32_t* x) {
             return make_uint4(x[0] | x[1] << 16, x[2] | x[3] << 16, x[4] | x[5] << 16,
@@ -175,7 +264,8 @@ __global__ __launch_bounds__(kThreads) void split_a_row_kernel(int m, int k, int
 
 struct SbParams {
     int m, n, k, k_span, m_pad, k_pad;
-    const uint16_t* A3;  // the three planes (pre-pass), or
+    const uint16_t* A3;  // the three planes (pre-pass) and their rows' shifts, or
+    const int* shifts;
     const float* A;      // fp32 A, split in registers (RAW kernels)
     const int8_t* B;
     const float* scale;
@@ -207,6 +297,62 @@ __device__ __forceinline__ void rope_store(const SbParams& p, int row, int c, fl
     }
 }
 
+// One 16-row block of split_bf16_kernel's tile (columns c0 .. c0 + 255,
+// rows m0 .. m0 + 15, k in [kb, ke)) by fp32 multiply-adds of a * q, for a
+// block whose A the three-term split cannot hold (values below 2^-110, or
+// non-finite): fp32 products of such values keep their relative precision,
+// and inf * q gives +-inf (NaN at q = 0) as fp32 arithmetic does. Each lane
+// takes four adjacent columns (one 32-bit word of B per k) and every fourth
+// row (rows w, w + 4, ...; the A values of a row are the same in every lane
+// of the wave). Output as the kernel's epilogue writes it: scaled into C
+// (with the accumulation or the RoPE epilogue) or unscaled into the
+// partials. Slow (16 multiply-adds per lane per k), small in registers.
+__device__ __forceinline__ void fma_block(const SbParams& p, int c0, int m0, int kb, int ke,
+                                          int slice) {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int c = c0 + 4 * (threadIdx.x % kWave);
+    const bool live = c < p.n;  // n % 16 == 0: all four columns or none
+    const int8_t* b = p.B + (live ? c : 0);
+    const float* a_row[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        a_row[i] = p.A + static_cast<std::size_t>(min(m0 + 4 * i + w, p.m - 1)) * p.k;
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[i][e] = 0.0f;
+    for (int kk = kb; kk < ke; ++kk) {
+        float q[4];
+        widen4(*reinterpret_cast<const uint32_t*>(b + static_cast<std::size_t>(kk) * p.n), q);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float a = a_row[i][kk];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][e] = fmaf(a, q[e], acc[i][e]);
+        }
+    }
+    if (!live) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = m0 + 4 * i + w;
+        if (row >= p.m) break;
+        floatx4 v{acc[i][0], acc[i][1], acc[i][2], acc[i][3]};
+        if (p.direct) {
+            v *= *reinterpret_cast<const floatx4*>(p.scale + c);
+            if (p.rope.pos) {
+                rope_store(p, row, c, v);
+                continue;
+            }
+            floatx4* o = reinterpret_cast<floatx4*>(p.out + static_cast<std::size_t>(row) * p.n + c);
+            *o = p.accumulate ? *o + v : v;
+        } else {
+            *reinterpret_cast<floatx4*>(
+                p.out + (static_cast<std::size_t>(slice) * p.m + row) * p.n + c) = v;
+        }
+    }
+}
+
 template <int RB, bool RAW>
 struct Chunk {
     uint4 b[8];         // rows 8g + e of the chunk, 16 columns each
@@ -224,8 +370,11 @@ struct Chunk<RB, true> {
 // Eight fp32 values -> the three bf16 terms, packed as MFMA A operands: the
 // split3 arithmetic, with each term's top halves paired by one byte permute
 // (4.5 VALU ops per value; the MFMA pipe does not hide VALU work, so this
-// count sets the kernel's speed as much as the MFMAs do).
-__device__ __forceinline__ void split8(const floatx4& x0, const floatx4& x1, uint4 (&t)[3]) {
+// count sets the kernel's speed as much as the MFMAs do). The lo remainders
+// are ORed into `lost`, whose low half is then non-zero iff some lo term
+// dropped bits (half an op per value); an infinite value gives a NaN sum.
+__device__ __forceinline__ void split8(const floatx4& x0, const floatx4& x1, uint4 (&t)[3],
+                                       uint32_t& lost) {
 #pragma clang fp contract(off)
     const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
     uint32_t a[8], r1[8], r2[8];
@@ -236,6 +385,8 @@ __device__ __forceinline__ void split8(const floatx4& x0, const floatx4& x1, uin
         r1[e] = bits(f1);
         r2[e] = bits(f1 - from_bits(r1[e] & 0xffff0000u));
     }
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) lost = lost | r2[e] | r2[e + 1];
     auto pair = [](const uint32_t* x, int e) {
         return __builtin_amdgcn_perm(x[e + 1], x[e], 0x07060302u);  // top halves, x[e] low
     };
@@ -341,15 +492,20 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
     // Column t + 1 is widened while column t's MFMAs run; the barriers pin
     // that order (left alone, the scheduler puts each widening right before
     // its MFMAs, which then wait on it).
+    // RAW: low half non-zero once a lo term of this lane's A row 16 rb + j
+    // dropped bits.
+    uint32_t lost[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) lost[rb] = 0;
     auto multiply = [&](const Chunk<RB, RAW>& c) {
         uint4 aop[RB][3];
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
             if constexpr (RAW && !WHOLE) {
                 const floatx4 z{0.f, 0.f, 0.f, 0.f};
-                split8(c.aok ? c.a[rb][0] : z, c.aok ? c.a[rb][1] : z, aop[rb]);
+                split8(c.aok ? c.a[rb][0] : z, c.aok ? c.a[rb][1] : z, aop[rb], lost[rb]);
             } else if constexpr (RAW) {
-                split8(c.a[rb][0], c.a[rb][1], aop[rb]);
+                split8(c.a[rb][0], c.a[rb][1], aop[rb], lost[rb]);
             } else {
 #pragma unroll
                 for (int term = 0; term < 3; ++term) aop[rb][term] = c.a[rb][term];
@@ -393,8 +549,13 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
 
     // Epilogue, one 16-row block at a time: wave sums into LDS by actual
     // column, then each thread adds the four waves for 16 consecutive
-    // columns of one row and writes four float4.
+    // columns of one row and writes four float4. RAW: a block where a lo
+    // term dropped bits (|a| below 2^-110) or a sum is not finite (an
+    // infinite or NaN activation, or an overflow) is not written here but
+    // computed again by fma_block once the others are out.
     const int orow = tid / 16, ocol = (tid % 16) * 16;
+    __shared__ int any_bad[4];
+    uint32_t redo = 0;  // RAW: bit rb set for each block fma_block recomputes
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
         if (rb > 0) __syncthreads();
@@ -405,29 +566,67 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
             for (int r = 0; r < 4; ++r) mine[(4 * g + r) * kTileStride + 16 * j + t] = acc[rb][t][r];
         __syncthreads();
         const int row = m0 + 16 * rb + orow;
+        floatx4 v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            // (Columns past n are in the tile too; their sums go nowhere.)
+            v[q] = *reinterpret_cast<const floatx4*>(&tile[orow * kTileStride + ocol + 4 * q]);
+#pragma unroll
+            for (int ww = 1; ww < 4; ++ww)
+                v[q] += *reinterpret_cast<const floatx4*>(
+                    &tile[(ww * 16 + orow) * kTileStride + ocol + 4 * q]);
+        }
+        if constexpr (RAW) {
+            bool bad = (lost[rb] & 0xffffu) != 0;
+            if (row < p.m) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        bad |= c0 + ocol + 4 * q < p.n && !(fabsf(v[q][e]) < __builtin_inff());
+            }
+            const bool wave_bad = __ballot(bad) != 0;
+            if (lane == 0) any_bad[w] = wave_bad;
+            __syncthreads();
+            if (__builtin_amdgcn_readfirstlane(any_bad[0] | any_bad[1] | any_bad[2] | any_bad[3])) {
+                redo |= 1u << rb;
+                continue;
+            }
+        }
         if (row < p.m) {
+            // Pre-split planes: the row's scale undone, after the column
+            // scale into C, before it into the partials (reduce_slices
+            // applies it).
+            const int sh = RAW ? 0 : -p.shifts[row];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int c = c0 + ocol + 4 * q;
                 if (c >= p.n) break;
-                floatx4 v = *reinterpret_cast<const floatx4*>(&tile[orow * kTileStride + ocol + 4 * q]);
+                floatx4 x = v[q];
+                if (p.direct) x *= *reinterpret_cast<const floatx4*>(p.scale + c);
+                if constexpr (!RAW) {
 #pragma unroll
-                for (int ww = 1; ww < 4; ++ww)
-                    v += *reinterpret_cast<const floatx4*>(
-                        &tile[(ww * 16 + orow) * kTileStride + ocol + 4 * q]);
+                    for (int e = 0; e < 4; ++e) x[e] = __builtin_ldexpf(x[e], sh);
+                }
                 if (p.direct) {
-                    v *= *reinterpret_cast<const floatx4*>(p.scale + c);
                     if (p.rope.pos) {
-                        rope_store(p, row, c, v);
+                        rope_store(p, row, c, x);
                         continue;
                     }
                     floatx4* o = reinterpret_cast<floatx4*>(p.out + static_cast<std::size_t>(row) * p.n + c);
-                    *o = p.accumulate ? *o + v : v;
+                    *o = p.accumulate ? *o + x : x;
                 } else {
                     *reinterpret_cast<floatx4*>(
-                        p.out + (static_cast<std::size_t>(place.slice) * p.m + row) * p.n + c) = v;
+                        p.out + (static_cast<std::size_t>(place.slice) * p.m + row) * p.n + c) = x;
                 }
             }
+        }
+    }
+    if constexpr (RAW) {
+        while (redo) {
+            const int rb = __builtin_ctz(redo);
+            redo &= redo - 1;
+            fma_block(p, c0, m0 + 16 * rb, kb, ke, place.slice);
         }
     }
 }
@@ -513,14 +712,18 @@ bool run_split_bf16(const MatmulArgs& a, const RopeFuse* rope) {
     const int k_pad = ceil_div(a.k, kChunk) * kChunk;
 
     uint16_t* A3 = nullptr;
+    int* shifts = nullptr;
     if (!raw) {
-        A3 = reinterpret_cast<uint16_t*>(
-            scratch(kSplitA, (static_cast<std::size_t>(3) * m_pad * k_pad + 1) / 2));
+        // The planes, then one int per row: its power-of-two shift.
+        const std::size_t plane_floats = (static_cast<std::size_t>(3) * m_pad * k_pad + 1) / 2;
+        float* base = scratch(kSplitA, plane_floats + m_pad);
+        A3 = reinterpret_cast<uint16_t*>(base);
+        shifts = reinterpret_cast<int*>(base + plane_floats);
         const int steps = ceil_div(k_pad, 8 * kThreads);
         const int vec4 = a.k % 4 == 0 && reinterpret_cast<uintptr_t>(a.A) % 16 == 0;
         auto row = [&](auto kern) {
             hipLaunchKernelGGL(kern, dim3(m_pad), dim3(kThreads), 0, a.stream, a.m, a.k, m_pad,
-                               k_pad, vec4, a.A, a.rms_weight, A3);
+                               k_pad, vec4, a.A, a.rms_weight, A3, shifts);
         };
         if (steps <= 1) {
             row(split_a_row_kernel<1>);
@@ -530,7 +733,7 @@ bool run_split_bf16(const MatmulArgs& a, const RopeFuse* rope) {
             row(split_a_row_kernel<4>);
         } else {
             hipLaunchKernelGGL(split_a_kernel, dim3(m_pad), dim3(kThreads), 0, a.stream, a.m, a.k,
-                               m_pad, k_pad, a.A, a.rms_weight, A3);
+                               m_pad, k_pad, a.A, a.rms_weight, A3, shifts);
         }
     }
 
@@ -549,6 +752,7 @@ bool run_split_bf16(const MatmulArgs& a, const RopeFuse* rope) {
     p.m_pad = m_pad;
     p.k_pad = k_pad;
     p.A3 = A3;
+    p.shifts = shifts;
     p.A = a.A;
     p.B = static_cast<const int8_t*>(a.B);
     p.scale = a.scale;

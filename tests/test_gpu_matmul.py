@@ -363,6 +363,12 @@ def test_config5_llama7b_projections(name):
     rows = np.array([0, 1, 77, 255, 256, 400, 510, 511])
     exact = orc.matmul_f64(A[rows], Wd)
     assert np.all(np.abs(got[rows] - exact) <= 1e-4 * orc.abs_bound(A[rows], Wd))
+    # The whole C against the reference's matmul_parallel(A, QTensor) at the
+    # reference tests' 1e-5 * k, as config 3 does (oracle/_ref present).
+    ref = oracle.ref()
+    if ref is not None:
+        want = ref.matmul_q8(A, qh, sh)
+        assert np.abs(got - want).max() <= 1e-5 * k
 
 
 @pytest.mark.parametrize("N", [1024, 2048, 4096])
@@ -457,6 +463,96 @@ def test_exact_split_tighter_than_fp32_tolerance(shape):
         ratio = float((np.abs(got - exact) / np.maximum(bound, 1e-300)).max())
         print(f"{shape} {kernel}: max |err| / sum|a||w| = {ratio:.2e}")
         assert ratio <= 1e-5, (kernel, ratio)
+
+
+def ranged_rows(m, k, seed):
+    """Rows of A that stress the three-term split, each row one class:
+    log-uniform over 1e-38 .. 1e-30 (remainders far below fp32's normal
+    range), one magnitude near 1e-37 (every value's low bits subnormal),
+    fp32's smallest normals (2^-126 and just above), subnormals (1.5e-45 ..
+    1e-38), and mixed over 1e-38 .. 1e20; signs random."""
+    ln_ranges = [(np.log(1e-38), np.log(1e-30)), (-85.2, -85.2 + 0.7),
+                 (np.log(2.0 ** -126), np.log(2.0 ** -126) + 0.05),
+                 (np.log(1.5e-45), np.log(1e-38)), (np.log(1e-38), np.log(1e20))]
+    rows = []
+    for r in range(m):
+        a, b = ln_ranges[r % len(ln_ranges)]
+        mag = np.exp(inputs.uniform((k,), a, b, seed + r).astype(np.float64)).astype(np.float32)
+        sign = np.where(inputs.uniform((k,), -1.0, 1.0, seed + 7919 + r) < 0, -1.0, 1.0)
+        rows.append((mag * sign).astype(np.float32))
+    return np.stack(rows).astype(np.float32)
+
+
+# k a multiple of 8 (A split in registers), ragged k (pre-split planes), one
+# 16-row block and several, a split k.
+RANGE_SHAPES = [(16, 4096, 512), (12, 1029, 256), (64, 4096, 4096), (40, 300, 272),
+                (512, 4096, 512), (9, 8192, 64)]
+
+
+@pytest.mark.parametrize("shape", RANGE_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_exact_split_tiny_magnitudes(shape):
+    # Each row's sum against the f64 product within 1e-4 * sum|a||w|, with
+    # and without the fused norm (the pre-pass path). A C element may round
+    # into fp32's subnormal range, where its spacing is 2^-149: that much
+    # absolute slack is allowed, the reference's fp32 sum has no less.
+    # The fused norm sums squares in fp32, as the reference's CUDA norm does
+    # (cuda_matmul.cu:162-170,256-266; its CPU rmsnorm sums in double): a
+    # row whose sum of squares passes fp32's range (values past ~1.8e19)
+    # gets scale 1 / sqrt(inf) = 0 and a zero row of C there, which is what
+    # is checked for it.
+    m, k, n = shape
+    A = ranged_rows(m, k, 531)
+    q, s = orc.quantize_q8(inputs.normal((k, n), 0.02, 532))
+    Bf = orc.dequantize(q, s)
+    w = inputs.uniform((k,), 0.5, 1.5, 533)
+    floor = 2.0 ** -149
+    ss = (A.astype(np.float64) ** 2).sum(axis=1)
+    fits = ss < float(np.finfo(np.float32).max)
+    assert fits.sum() >= m // 2 and (~fits).any()
+    for kernel in ("automatic", "tiled_split"):
+        for norm in (False, True):
+            rows = fits if norm else np.ones(m, bool)
+            Ause = orc.rmsnorm(A[rows], w) if norm else A
+            exact = orc.matmul_f64(Ause, Bf)
+            bound = orc.abs_bound(Ause, Bf)
+            got = host(em.matmul(dev(A), dev(q), scale=dev(s), kernel=kernel,
+                                 rms_weight=dev(w) if norm else None)).astype(np.float64)
+            err = np.abs(got[rows] - exact)
+            ratio = float((err / np.maximum(bound, 1e-300)).max())
+            print(f"{shape} {kernel} norm={norm}: max |err| / sum|a||w| = {ratio:.2e}")
+            assert np.all(err <= 1e-4 * bound + floor), (kernel, norm, ratio)
+            if norm:
+                assert np.all(got[~rows] == 0.0), kernel
+
+
+@pytest.mark.parametrize("shape", [(16, 4096, 512), (12, 1029, 256)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_exact_split_infinities_pass_through(shape):
+    # An infinite activation gives +-inf in every column where its weight is
+    # non-zero and NaN where it is zero (inf * 0), as fp32 arithmetic and the
+    # reference's CPU product do; rows without one stay finite and within
+    # the bound. A NaN activation makes its row NaN.
+    m, k, n = shape
+    A = inputs.normal((m, k), 1.0, 541)
+    A[1, 5] = np.inf
+    A[3, 7] = -np.inf
+    A[5, 3] = np.inf
+    A[5, k - 1] = -np.inf  # both signs in one row: NaN where both weights are non-zero
+    A[7, 100] = np.nan
+    q, s = orc.quantize_q8(inputs.normal((k, n), 0.02, 542))
+    q[5, :n // 4] = 0  # inf * 0 columns
+    Bf = orc.dequantize(q, s)
+    with np.errstate(invalid="ignore", over="ignore"):
+        want = A.astype(np.float64) @ Bf.astype(np.float64)
+    finite_rows = [r for r in range(m) if np.all(np.isfinite(A[r]))]
+    bound = orc.abs_bound(A[finite_rows], Bf)
+    for kernel in ("automatic", "tiled_split"):
+        got = host(em.matmul(dev(A), dev(q), scale=dev(s), kernel=kernel)).astype(np.float64)
+        assert np.array_equal(np.isnan(got), np.isnan(want)), kernel
+        assert np.array_equal(np.isposinf(got), np.isposinf(want)), kernel
+        assert np.array_equal(np.isneginf(got), np.isneginf(want)), kernel
+        err = np.abs(got[finite_rows] - want[finite_rows])
+        assert np.all(err <= 1e-4 * bound), kernel
 
 
 @pytest.mark.parametrize("shape", [(40, 1000, 304), (256, 1000, 16384), (300, 4096, 512),

@@ -181,6 +181,38 @@ def test_decode_merge_inside_wo_gemv(tmp_path, monkeypatch, dim, hidden, heads, 
     merged_first.close()
 
 
+@pytest.mark.parametrize("heads,kv_heads", [(4, 4), (4, 2)], ids=["mha", "gqa"])
+def test_prefill_rope_epilogue_same_bits_as_rope_kernel(tmp_path, monkeypatch, heads, kv_heads):
+    # Int8 prefill rows send the fused qkv product to the exact-split kernel;
+    # with no k split (k = dim = 256 here) it rotates q and k and writes the
+    # caches in its epilogue. A second model created with
+    # EM_PREFILL_ROPE_FUSION=0 writes qkv and runs rope_cache_kernel
+    # instead. Every logit must be the same bits: prefill from 0, a second
+    # prefill chunk from position 40 (angles taken at pos + row) and decode
+    # steps that read the caches both wrote. Against the CPU Transformer too.
+    m = e2e_model.fixture_model(heads, kv_heads, False, seed=300 + heads + kv_heads, dim=256,
+                                hidden=688, vocab=300, seq_len=128)
+    path = str(tmp_path / "model.bin")
+    e2e_model.write_raw(path, m)
+    ck = oracle.RefCheckpoint(lib, path)
+    w = ck.weights()
+    cpu = oracle.RefTransformer(lib, ck, True)
+    fused = em.Model(ck.config, w, q8=True)
+    monkeypatch.setenv("EM_PREFILL_ROPE_FUSION", "0")
+    plain = em.Model(ck.config, w, q8=True)
+    monkeypatch.delenv("EM_PREFILL_ROPE_FUSION")
+    V = ck.config["vocab_size"]
+    tokens = [(p * 17 + 3) % V for p in range(100)]
+    steps = [(tokens[:40], 0), (tokens[40:72], 40)] + [([tokens[p]], p) for p in range(72, 80)]
+    for part, pos in steps:
+        a, b = fused.forward(part, pos), plain.forward(part, pos)
+        assert np.array_equal(a, b), f"{len(part)} rows at {pos}: max diff {np.abs(a - b).max()}"
+        c = cpu.run(part, pos, len(part) == 1)
+        assert float(np.abs(a - c).max()) <= 1e-4 * float(np.abs(c).max()), f"at {pos}"
+    fused.close()
+    plain.close()
+
+
 def test_bad_inputs_then_cache_still_works(tmp_path):
     ck, w = load(tmp_path, 4, 2, True)
     gpu = em.Model(ck.config, w)
