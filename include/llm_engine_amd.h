@@ -90,6 +90,23 @@ int em_matmul_q8(size_t m, size_t n, size_t k, const float* A, const int8_t* B,
                  const float* scale, float* C, int kernel, int accumulate,
                  const float* rms_weight, void* stream);
 
+/* em_matmul_q8 with EM_KERNEL_SKINNY (m <= 8), allocating nothing: for
+ * callers that cannot call hipMalloc (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid it). The GEMV's split-K partials go
+ * to a 32 MiB device array the library holds on each GPU until the process
+ * ends, instead of grow-only scratch; results are the same bits as
+ * em_matmul_q8 with EM_KERNEL_SKINNY (registered weights included), and
+ * em_scratch_generation() does not move. EM_EINVAL, before any launch, for
+ * what em_matmul_q8 rejects and for a shape whose partials need more than
+ * 32 MiB (every Llama-7B-shaped product up to 8 rows fits: 8 rows of the
+ * 4096 x 32000 classifier need 31.25 MiB). Every call on a GPU shares
+ * that GPU's array: calls that overlap on one GPU (other streams, other
+ * host threads) race; calls on one stream are ordered. No counterpart in
+ * the reference. */
+int em_matmul_q8_noalloc(size_t m, size_t n, size_t k, const float* A, const int8_t* B,
+                         const float* scale, float* C, int accumulate, const float* rms_weight,
+                         void* stream);
+
 /* ---- Strip layout of int8 weights (explicit opt-in) ------------------------
  * The reference keeps int8 weights row-major (QTensor, tensor.h:23-28); the
  * entry points above take that layout. The strip layout is an opt-in copy for

@@ -28,7 +28,7 @@ STREAM_PER_THREAD = 2
 EXPORTS = (
     "em_last_error", "em_available", "em_synchronize", "em_scratch_generation",
     "em_malloc", "em_free", "em_memcpy_h2d", "em_memcpy_d2h",
-    "em_matmul_f32", "em_matmul_q8", "em_quantize_q8", "em_dequantize_q8", "em_stream_read",
+    "em_matmul_f32", "em_matmul_q8", "em_matmul_q8_noalloc", "em_quantize_q8", "em_dequantize_q8", "em_stream_read",
     "em_probe_empty", "em_probe_read", "em_probe_gemv_q8",
     "em_pack_q8", "em_unpack_q8", "em_matmul_q8_packed",
     "em_q8_register", "em_q8_unregister", "em_q8_registered",
@@ -120,6 +120,8 @@ def lib() -> ctypes.CDLL:
                                     _vp, _vp]
         L.em_matmul_q8.argtypes = [_sz, _sz, _sz, _vp, _vp, _vp, _vp, ctypes.c_int,
                                    ctypes.c_int, _vp, _vp]
+        L.em_matmul_q8_noalloc.argtypes = [_sz, _sz, _sz, _vp, _vp, _vp, _vp, ctypes.c_int, _vp,
+                                           _vp]
         L.em_quantize_q8.argtypes = [_sz, _sz, _vp, _vp, _vp, _vp]
         L.em_dequantize_q8.argtypes = [_sz, _sz, _vp, _vp, _vp, _vp]
         L.em_stream_read.argtypes = [_vp, _sz, _vp, _vp]
@@ -195,6 +197,12 @@ def matmul_q8_raw(m, n, k, A, B, scale, C, kernel="automatic", accumulate=False,
                               int(bool(accumulate)), rms_weight, stream))
 
 
+def matmul_q8_noalloc_raw(m, n, k, A, B, scale, C, accumulate=False, rms_weight=None,
+                          stream=None) -> None:
+    _check(lib().em_matmul_q8_noalloc(m, n, k, A, B, scale, C, int(bool(accumulate)),
+                                      rms_weight, stream))
+
+
 def quantize_q8_raw(rows, cols, B, q, scale, stream=None) -> None:
     _check(lib().em_quantize_q8(rows, cols, B, q, scale, stream))
 
@@ -237,6 +245,23 @@ def matmul(A, B, C=None, *, scale=None, kernel="automatic", accumulate=False, rm
     else:
         matmul_f32_raw(m, n, k, _dev(A, torch.float32), _dev(B, torch.float32),
                        _dev(C, torch.float32), kernel, accumulate, rw, s)
+    return C
+
+
+def matmul_q8_noalloc(A, B, C, scale, *, accumulate=False, rms_weight=None, stream=None):
+    """em_matmul_q8_noalloc: C = [C +] rmsnorm?(A) x dequantize(B, scale) for
+    m <= 8 rows through the skinny GEMV, its split-K partials in the
+    library's static per-GPU scratch (nothing allocated). C is given."""
+    import torch
+    m, k = A.shape
+    n = B.shape[1]
+    if B.shape[0] != k or tuple(C.shape) != (m, n):
+        raise InvalidArgument(EM_EINVAL, f"matmul_q8_noalloc: shapes differ (A is {m}x{k}, "
+                                         f"B is {B.shape[0]}x{n}, C is {tuple(C.shape)})")
+    rw = _dev(rms_weight, torch.float32) if rms_weight is not None else None
+    matmul_q8_noalloc_raw(m, n, k, _dev(A, torch.float32), _dev(B, torch.int8),
+                          _dev(scale, torch.float32), _dev(C, torch.float32), accumulate, rw,
+                          _stream_ptr(stream))
     return C
 
 

@@ -72,10 +72,17 @@ const int8_t* strip_copy_of(const void* B, std::size_t k, std::size_t n) {
 // with m and the row-major kernels win.
 constexpr std::size_t kStripMaxK = 8192;
 
+}  // namespace
+
+// The matmul entry points. `workspace` (em_matmul_q8_noalloc, with the
+// skinny kernel): called once the shape is valid and a GPU is present, it
+// returns the caller's buffer for split-K partials and its size in floats;
+// the product then allocates nothing, and a shape whose partials do not fit
+// is rejected before any launch.
 template <class BT>
 int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, const BT* B,
                  const float* scale, float* C, int kernel, int accumulate,
-                 const float* rms_weight, void* stream) {
+                 const float* rms_weight, void* stream, Workspace workspace) {
     if (kernel < EM_KERNEL_AUTOMATIC || kernel > EM_KERNEL_SKINNY)
         return fail(EM_EINVAL, "matmul_cuda: unknown kernel " + std::to_string(kernel));
     // automatic: skinny up to 8 rows, as the reference (cuda_matmul.cu:406-410).
@@ -104,6 +111,12 @@ int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, co
     if (std::is_same<BT, int8_t>::value && k && !scale)
         return fail(EM_EINVAL, "matmul_cuda: int8 B needs its column scales " + shapes(m, n, k));
     if (!device_present()) return fail(EM_ENODEV, "matmul_cuda: no usable GPU");
+    float* ws = nullptr;
+    std::size_t ws_floats = 0;
+    if (workspace) {
+        ws = workspace(&ws_floats);
+        if (!ws) return EM_EDEVICE;  // workspace() set the message
+    }
 
     hipStream_t s = static_cast<hipStream_t>(stream);
     try {
@@ -157,7 +170,19 @@ int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, co
                     run_tiled<BT>(a);
                 }
                 break;
-            default: run_skinny<BT>(a); break;
+            default:
+                if (ws) {
+                    const std::size_t need = skinny_partial_floats<BT>(a);
+                    if (need > ws_floats)
+                        return fail(EM_EINVAL, "matmul_q8_noalloc: split-K partials need " +
+                                                   std::to_string(need * sizeof(float)) +
+                                                   " bytes, more than the static scratch's " +
+                                                   std::to_string(ws_floats * sizeof(float)) +
+                                                   " " + shapes(m, n, k));
+                    a.partials = ws;
+                }
+                run_skinny<BT>(a);
+                break;
         }
         hip_check(hipGetLastError(), "launch");
     } catch (const DeviceError& e) {
@@ -168,7 +193,12 @@ int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, co
     return EM_OK;
 }
 
-}  // namespace
+template int matmul_entry<float>(std::size_t, std::size_t, std::size_t, const float*,
+                                 const float*, const float*, float*, int, int, const float*,
+                                 void*, Workspace);
+template int matmul_entry<int8_t>(std::size_t, std::size_t, std::size_t, const float*,
+                                  const int8_t*, const float*, float*, int, int, const float*,
+                                  void*, Workspace);
 
 int fail(int code, const std::string& msg) {
     g_error = msg;

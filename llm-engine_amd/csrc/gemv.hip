@@ -612,10 +612,15 @@ int rows_per_lane(int E, int m, int n, int k) {
     return L < cap ? L : cap;
 }
 
-}  // namespace
+// The GEMV's lane width E (16 int8 or 4 fp32 columns per 16-byte load, 1
+// for widths or alignments that rule those out), rows per lane L and k
+// slices for a product.
+struct SkinnyLayout {
+    int E, L, slices;
+};
 
 template <class BT>
-int run_skinny_partials(const MatmulArgs& a, const float** partial) {
+SkinnyLayout skinny_layout(const MatmulArgs& a) {
     const BT* B = static_cast<const BT*>(a.B);
     int E = 1;
     if (std::is_same<BT, int8_t>::value && a.n % 16 == 0 && aligned(B, 16)) {
@@ -625,7 +630,22 @@ int run_skinny_partials(const MatmulArgs& a, const float** partial) {
     }
     const int L = rows_per_lane(E, a.m, a.n, a.k);
     const int rows_per_block = E * (E == 1 ? 16 : L);
-    const int slices = ceil_div(a.k, rows_per_block);
+    return {E, L, ceil_div(a.k, rows_per_block)};
+}
+
+}  // namespace
+
+template <class BT>
+std::size_t skinny_partial_floats(const MatmulArgs& a) {
+    const int slices = skinny_layout<BT>(a).slices;
+    return slices > 1 ? static_cast<std::size_t>(slices) * a.m * a.n : 0;
+}
+
+template <class BT>
+int run_skinny_partials(const MatmulArgs& a, const float** partial) {
+    const BT* B = static_cast<const BT*>(a.B);
+    const SkinnyLayout lay = skinny_layout<BT>(a);
+    const int E = lay.E, L = lay.L, slices = lay.slices;
     const dim3 grid(ceil_div(a.n, kThreads), slices);
 
     GemvParams<BT> p{};
@@ -639,8 +659,9 @@ int run_skinny_partials(const MatmulArgs& a, const float** partial) {
     p.direct = slices == 1;
     p.a_vec4 = a.k % 4 == 0 && aligned(a.A, 16);
     p.accumulate = a.accumulate && p.direct;
-    p.out = p.direct ? a.C
-                     : scratch(kPartial, static_cast<size_t>(slices) * a.m * a.n);
+    p.out = p.direct      ? a.C
+            : a.partials ? a.partials
+                         : scratch(kPartial, static_cast<size_t>(slices) * a.m * a.n);
     p.ssq = a.ssq;
     p.ssq_parts = ceil_div(a.k, kSsqChunk);
     if (a.rms_weight && a.ssq && a.m == 1 && p.ssq_parts <= kSsqParts) {
@@ -808,6 +829,8 @@ bool run_skinny_probe(const MatmulArgs& a, int variant, int* counters) {
     return true;
 }
 
+template std::size_t skinny_partial_floats<float>(const MatmulArgs&);
+template std::size_t skinny_partial_floats<int8_t>(const MatmulArgs&);
 template int run_skinny_partials<float>(const MatmulArgs&, const float**);
 template int run_skinny_partials<int8_t>(const MatmulArgs&, const float**);
 template void run_skinny<float>(const MatmulArgs&);

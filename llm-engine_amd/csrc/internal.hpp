@@ -59,7 +59,20 @@ struct MatmulArgs {
     // values [64j, 64j + 64), j < ceil(k / 64), that A's producer left; the
     // norm is formed from them instead of from all of A in every workgroup.
     const float* ssq;
+    // GEMV only: the caller's buffer for the split-K partials (at least
+    // skinny_partial_floats() floats) in place of the library's scratch.
+    float* partials;
 };
+
+// em_matmul_f32 / em_matmul_q8 (api.hip): validation, dispatch, errors as
+// EM_* codes. `workspace`, when given (em_matmul_q8_noalloc), supplies the
+// buffer for the GEMV's split-K partials and its size in floats, or returns
+// null with the error message set.
+using Workspace = float* (*)(std::size_t* floats);
+template <class BT>
+int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, const BT* B,
+                 const float* scale, float* C, int kernel, int accumulate,
+                 const float* rms_weight, void* stream, Workspace workspace = nullptr);
 
 // Decode-shaped GEMV, m <= 8 (GpuKernel::skinny). Fuses the norm.
 template <class BT>
@@ -71,6 +84,10 @@ void run_skinny(const MatmulArgs& a);
 // reduce_slices does (a consumer kernel that fuses the sum).
 template <class BT>
 int run_skinny_partials(const MatmulArgs& a, const float** partial);
+// The floats of split-K partials run_skinny_partials(a) writes (0 when it
+// needs one k slice and writes C itself).
+template <class BT>
+std::size_t skinny_partial_floats(const MatmulArgs& a);
 // One row of silu_mul(gate, up) x B, the gate | up product (split at
 // `hidden` = k) given as a Summed with at most 16 slices: the forward pass's
 // SwiGLU formed inside the GEMV's A staging, C (+)= as run_skinny writes

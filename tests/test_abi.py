@@ -87,6 +87,21 @@ def test_no_device_is_reported():
     assert em.scratch_generation() == 0
 
 
+def test_noalloc_checks_before_the_gpu():
+    # em_matmul_q8_noalloc validates as em_matmul_q8 with the skinny kernel,
+    # on the host, before it looks for the device's static scratch.
+    e = err(lambda: em.matmul_q8_noalloc_raw(9, 2, 2, 16, 16, 16, 16))
+    assert e.code == em.EM_EINVAL and "at most 8 rows" in str(e)
+    e = err(lambda: em.matmul_q8_noalloc_raw(2, 3, 4, 16, 16, None, 16))
+    assert e.code == em.EM_EINVAL and "scales" in str(e)
+    e = err(lambda: em.matmul_q8_noalloc_raw(2, 3, 1 << 30, 16, 16, 16, 16))
+    assert e.code == em.EM_EINVAL and "2^31" in str(e)
+    em.matmul_q8_noalloc_raw(0, 3, 4, None, None, None, None)  # empty: a no-op
+    if not em.available():
+        assert err(lambda: em.matmul_q8_noalloc_raw(1, 16, 16, 16, 16, 16, 16)).code == \
+            em.EM_ENODEV
+
+
 def test_skinny_check_precedes_size_check():
     # As in matmul_impl: kernel choice, then the skinny row limit, then 2^31.
     e = err(lambda: em.matmul_f32_raw(9, 1 << 16, 1 << 16, 16, 16, 16, "skinny"))
