@@ -573,6 +573,28 @@ def profile_split_pass(em, torch, m: int = 512, reps: int = 20) -> dict:
     return {"m": m, "launches": reps, "flops_per_launch": 2 * m * DIM * DIM}
 
 
+# The Llama-7B layer's four projections at a 512-row prefill: (k, n, norm).
+LLAMA7B_PROJ = [(4096, 12288, True), (4096, 4096, False), (4096, 22016, True),
+                (11008, 4096, False)]
+
+
+def profile_proj_pass(em, torch, m: int = 512, reps: int = 5) -> dict:
+    """Eager int8 products of the Llama-7B layer's projections at m rows
+    (`automatic`: the exact-split kernel; qkv and w13 with the norm fused, so
+    A is pre-split), two weight copies alternating, `reps` launches each,
+    for counter passes over the prefill kernels."""
+    for (k, n, norm) in LLAMA7B_PROJ:
+        pool = Pool(em, torch, True, k, n, 2, 2000 + n)
+        A = torch.randn((m, k), device="cuda")
+        C = torch.empty((m, n), device="cuda")
+        w = torch.rand((k,), device="cuda") + 0.5 if norm else None
+        for i in range(reps):
+            em.matmul(A, pool.ws[i % 2], C, scale=pool.scales[i % 2], rms_weight=w)
+        torch.cuda.synchronize()
+        pool.close()
+    return {"m": m, "shapes": LLAMA7B_PROJ, "launches_each": reps}
+
+
 def profile_prefill_pass(em, torch, reps: int = 5) -> dict:
     """Eager 512-token prefills of the two-layer Llama-7B-shaped model
     (llama7b_model), for rocprofv3 kernel traces of the forward pass."""
@@ -873,11 +895,11 @@ def main() -> int:
                     help="only the floor study of the headline call (empty launches, "
                          "16 MiB and 600 MiB read sweeps, single-launch GEMV variants)")
     ap.add_argument("--profile-pass", nargs="?", const="gemv",
-                    choices=["gemv", "gemm", "split", "smallm", "prefill", "decode"],
+                    choices=["gemv", "gemm", "split", "smallm", "proj", "prefill", "decode"],
                     help="eager launches for rocprofv3 --pmc: gemv (calibration copy + "
                          "headline, the default), gemm (fp32 tiled N=4096), split "
-                         "(int8 m=512, exact-split), prefill or decode (Llama-7B-shaped, "
-                         "2 layers)")
+                         "(int8 m=512, exact-split), smallm (int8 m=4/16/64), proj (the Llama-7B "
+                         "projections at m=512), prefill or decode (Llama-7B-shaped, 2 layers)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -914,6 +936,9 @@ def main() -> int:
         return 0
     if args.profile_pass == "smallm":
         print(json.dumps(profile_smallm_pass(em, torch)))
+        return 0
+    if args.profile_pass == "proj":
+        print(json.dumps(profile_proj_pass(em, torch)))
         return 0
     if args.profile_pass == "prefill":
         print(json.dumps(profile_prefill_pass(em, torch)))

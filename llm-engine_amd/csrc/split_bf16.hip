@@ -71,7 +71,12 @@ constexpr int kTile = 256;               // columns per workgroup
 constexpr int kChunk = 32;               // k rows per MFMA step of a wave
 constexpr int kStep = 4 * kChunk;        // the four waves' chunks
 constexpr int kDepth = 2;                // chunks in flight per wave
-constexpr int kTileStride = kTile + 4;   // LDS row stride of the epilogue tile
+// The epilogue tile in LDS: rows of kTile floats as 64 granules of four;
+// granule q of a row is stored at q ^ ((q >> 3) & 7). A lane's 16 columns
+// are granules 4j .. 4j + 3, so without the swizzle the 16-byte writes of
+// lanes j and j + 2 (and the reads of threads 16 columns apart) fall on the
+// same banks; with it, every eight consecutive lanes cover all 32 banks.
+__device__ __forceinline__ int granule(int q) { return q ^ ((q >> 3) & 7); }
 
 // --- A -> three bf16 planes -------------------------------------------------
 
@@ -417,7 +422,7 @@ __device__ __forceinline__ bf16x8 column(const uint4 (&b)[8], int t) {
 // lies inside k and no row or value needs a clamp or a mask.
 template <int RB, bool RAW, bool WHOLE>
 __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
-    __shared__ __attribute__((aligned(16))) float tile[4 * 16 * kTileStride];
+    __shared__ __attribute__((aligned(16))) floatx4 tile[4 * 16 * kTile / 4];
 
     const int tid = threadIdx.x;
     const int lane = tid % kWave;
@@ -559,22 +564,24 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
         if (rb > 0) __syncthreads();
-        float* mine = tile + w * 16 * kTileStride;
+        floatx4* mine = tile + w * 16 * (kTile / 4);
 #pragma unroll
-        for (int t = 0; t < 16; ++t)
+        for (int r = 0; r < 4; ++r)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) mine[(4 * g + r) * kTileStride + 16 * j + t] = acc[rb][t][r];
+            for (int q = 0; q < 4; ++q)
+                mine[(4 * g + r) * (kTile / 4) + granule(4 * j + q)] =
+                    floatx4{acc[rb][4 * q][r], acc[rb][4 * q + 1][r], acc[rb][4 * q + 2][r],
+                            acc[rb][4 * q + 3][r]};
         __syncthreads();
         const int row = m0 + 16 * rb + orow;
         floatx4 v[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             // (Columns past n are in the tile too; their sums go nowhere.)
-            v[q] = *reinterpret_cast<const floatx4*>(&tile[orow * kTileStride + ocol + 4 * q]);
+            const int gq = granule(ocol / 4 + q);
+            v[q] = tile[orow * (kTile / 4) + gq];
 #pragma unroll
-            for (int ww = 1; ww < 4; ++ww)
-                v[q] += *reinterpret_cast<const floatx4*>(
-                    &tile[(ww * 16 + orow) * kTileStride + ocol + 4 * q]);
+            for (int ww = 1; ww < 4; ++ww) v[q] += tile[(ww * 16 + orow) * (kTile / 4) + gq];
         }
         if constexpr (RAW) {
             bool bad = (lost[rb] & 0xffffu) != 0;
