@@ -575,6 +575,33 @@ def test_exact_split_fused_norm_and_accumulate(shape):
     check(host(C), want, An, orc.dequantize(q, s), k, factor=2.0, C0=C0)
 
 
+@pytest.mark.parametrize("norm", [True, False], ids=["norm", "plain"])
+def test_exact_split_last_round_as_two_block_tiles(norm):
+    # 512 x 4096 x 12288 with the norm: 384 four-block tiles, whose last
+    # round (128 tiles) runs as 256 two-block tiles in a second launch. Each
+    # element is summed in the same order either way, so the product equals,
+    # bit for bit, its column ranges computed as products of their own
+    # (8192 columns: four-block tiles; 4096: two-block), and the f64 product
+    # within 1e-4 * sum|a||w|. Without the norm the whole product takes
+    # two-block tiles (the same comparison, no second launch).
+    m, k, n = 512, 4096, 12288
+    A = dev(inputs.normal((m, k), 1.0, 551))
+    q, s = em.quantize_q8(dev(inputs.normal((k, n), 0.02, 552)))
+    w = dev(inputs.uniform((k,), 0.5, 1.5, 553)) if norm else None
+    whole = host(em.matmul(A, q, scale=s, rms_weight=w))
+    assert np.array_equal(whole, host(em.matmul(A, q, scale=s, rms_weight=w)))
+    for c0, c1 in ((0, 8192), (8192, 12288)):
+        part = host(em.matmul(A, q[:, c0:c1].contiguous(), scale=s[c0:c1].contiguous(),
+                              rms_weight=w))
+        assert np.array_equal(whole[:, c0:c1], part), (c0, c1)
+    rows = np.array([0, 63, 64, 255, 300, 511])
+    Ah = host(A)[rows]
+    An = orc.rmsnorm(Ah, host(w)) if norm else Ah
+    Wd = orc.dequantize(host(q), host(s))
+    exact = orc.matmul_f64(An, Wd)
+    assert np.all(np.abs(whole[rows] - exact) <= 1e-4 * orc.abs_bound(An, Wd))
+
+
 def test_stream_read_runs_and_checks_alignment():
     # The bench's read-only ceiling: one pass over a buffer, nothing written
     # but (almost never) the sink.
