@@ -52,9 +52,12 @@ def _run(cmd):
 # Per-file additions. attention.hip: the tile kernel rescales its MFMA
 # accumulators with VALU ops after every key block; in the default AGPR form
 # each rescale copies them out of and back into AGPRs (~300 moves per 128
-# MFMAs), so its MFMAs write VGPRs instead.
+# MFMAs), so its MFMAs write VGPRs instead. gemm_mfma.hip: in the AGPR form
+# the one-workgroup-per-CU build of the fp32 GEMM loop moved accumulators
+# between AGPRs and VGPRs (80 moves per 256 MFMAs).
 FILE_FLAGS = {
     "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "gemm_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

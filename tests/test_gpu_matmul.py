@@ -389,6 +389,27 @@ def test_config3_square_gemm(N):
         assert np.abs(got - want).max() <= 1e-5 * N
 
 
+# The streamlined fp32 tiled kernel (k % 32 == 0, n % 4 == 0): rows and
+# columns ending inside a 64 x 64 tile (out-of-range buffer loads must read
+# zeros and stores must stop), one row, k split over slices when the tile
+# grid is small (1 tile, k = 8192: 32 slices), accumulate into a non-zero C,
+# and a grid whose tile count is not a multiple of 8 (no XCD reordering).
+FAST_SHAPES = [(100, 96, 68), (1, 4096, 1028), (64, 8192, 64), (65, 32, 4),
+               (300, 1024, 700), (129, 2048, 1924), (7 * 64, 256, 5 * 64)]
+
+
+@pytest.mark.parametrize("shape", FAST_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_tiled_fast_kernel_edges(shape, accumulate):
+    m, k, n = shape
+    A, B = seeded(m, k, n, 77)
+    C0 = inputs.uniform((m, n), -1.0, 1.0, 79) if accumulate else np.zeros((m, n), np.float32)
+    C = dev(C0)
+    got = host(em.matmul(dev(A), dev(B), C, kernel="tiled", accumulate=accumulate))
+    want = orc.matmul_naive(A, B) + C0
+    check(got, want, A, B, k, C0=C0 if accumulate else None)
+
+
 # ------------------------------------------------- exact-split bf16 products
 
 # Covers one, two and four 16-row blocks per workgroup (m <= 256, < 1024,
