@@ -86,10 +86,10 @@ int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, co
     if (kernel < EM_KERNEL_AUTOMATIC || kernel > EM_KERNEL_SKINNY)
         return fail(EM_EINVAL, "matmul_cuda: unknown kernel " + std::to_string(kernel));
     // automatic: skinny up to 8 rows, as the reference (cuda_matmul.cu:406-410).
-    // Above that, the B-streaming fp32 MFMA kernel (tiled_split) at every m
-    // it supports: the reference switches to tiled past 64 rows, but on
-    // gfx950 tiled_split measured as fast or faster up to m = 4096 (within
-    // 2 % for fp32 at 4096^3). int8 B goes to the exact-split bf16 MFMA
+    // Above that, the B-streaming fp32 MFMA kernel (tiled_split), except
+    // where tiled_preferred picks the LDS-tiled GEMM (large m, small B, or
+    // wide B from 256 rows): the reference switches to tiled past 64 rows.
+    // int8 B goes to the exact-split bf16 MFMA
     // kernel instead (split_bf16.hip: at 4096^2, 1.1x faster than
     // tiled_split at m = 9-16 and 1.3-2.6x from m = 32 to 512), and so do
     // int8 products of fewer rows where it beats the GEMV
@@ -154,6 +154,8 @@ int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, co
             static_cast<long long>(n) * static_cast<long long>(k) >= (1LL << 25) &&
             tiled_split_supports<BT>(a))
             kernel = EM_KERNEL_TILED_SPLIT;
+        if (!std::is_same<BT, int8_t>::value && automatic && tiled_preferred(a))
+            kernel = EM_KERNEL_TILED;
         if (rms_weight && kernel != EM_KERNEL_SKINNY) {
             float* normed = scratch(kNorm, m * k);
             run_rmsnorm_rows(a.m, a.k, A, rms_weight, normed, s);

@@ -538,6 +538,12 @@ void run_fast(const MatmulArgs& a) {
     }
 }
 
+bool tiled_preferred(const MatmulArgs& a) {
+    if (a.m <= 8 || !fast_ok(a)) return false;
+    const long long kn = static_cast<long long>(a.k) * a.n;
+    return a.m >= 1024 || kn <= (1LL << 20) || (a.m >= 256 && a.n >= 2 * a.k);
+}
+
 template <class BT>
 void run_tiled(const MatmulArgs& a) {
     if (std::is_same<BT, float>::value && fast_ok(a)) {

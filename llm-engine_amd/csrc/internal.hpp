@@ -116,6 +116,15 @@ void run_tiled_split(const MatmulArgs& a);
 template <class BT>
 void run_tiled(const MatmulArgs& a);
 
+// True where automatic should run an fp32 product of more than 8 rows on the
+// tiled kernel rather than tiled_split: the streamlined tiled kernel takes
+// the shape and m >= 1024, or B has at most 2^20 values, or m >= 256 with
+// n >= 2k. Measured (us, tiled_split against tiled): 4096^2 at m = 1024
+// 267 / 253, m = 512 136 / 140; 4096 x 11008 at m = 256 263 / 197, m = 128
+// 135 / 140; 11008 x 4096 at m = 512 355 / 374, m = 1024 706 / 676;
+// 288 x 768 at m = 9 .. 1024 12-18 / 8.5; 768 x 288 at m = 32 16.2 / 11.8.
+bool tiled_preferred(const MatmulArgs& a);
+
 // One thread per element (GpuKernel::naive). A must already be normed.
 template <class BT>
 void run_naive(const MatmulArgs& a);
