@@ -564,16 +564,34 @@ def profile_smallm_pass(em, torch, reps: int = 20) -> dict:
     return {"m": [4, 16, 64], "launches_each": reps}
 
 
-def profile_gemm_pass(em, torch, N: int = 4096, reps: int = 5) -> dict:
-    """Eager fp32 GEMMs (`tiled`, N^3, the metric's second half) for rocprofv3
-    counter passes over the MFMA kernel: `reps` launches after 2 warm-ups."""
-    A = torch.rand((N, N), device="cuda") * 2 - 1
-    B = torch.rand((N, N), device="cuda") * 2 - 1
-    C = torch.empty((N, N), device="cuda")
-    for _ in range(2 + reps):
-        em.matmul(A, B, C, kernel="tiled")
-    torch.cuda.synchronize()
-    return {"gemm_N": N, "launches": 2 + reps, "flops_per_launch": 2 * N**3}
+def profile_gemm_pass(em, torch, reps: int = 5, warm_s: float = 0.3) -> dict:
+    """Eager fp32 GEMMs for rocprofv3 counter passes over the MFMA kernels: at
+    N = 1024, 2048 and 4096, `reps` launches of the library's `tiled` kernel
+    (N = 4096 is the metric's second half), then `reps` of torch.mm (the
+    vendor yardstick), each side after `warm_s` seconds of untimed launches
+    so the clock has settled."""
+    import time
+    torch.backends.cuda.matmul.allow_tf32 = False
+    done = {}
+    for N in (1024, 2048, 4096):
+        A = torch.rand((N, N), device="cuda") * 2 - 1
+        B = torch.rand((N, N), device="cuda") * 2 - 1
+        C = torch.empty((N, N), device="cuda")
+        for name, fn in (("tiled", lambda: em.matmul(A, B, C, kernel="tiled")),
+                         ("torch_mm", lambda: torch.mm(A, B, out=C))):
+            t0 = time.perf_counter()
+            warm = 0
+            while time.perf_counter() - t0 < warm_s:
+                fn()
+                torch.cuda.synchronize()
+                warm += 1
+            for _ in range(reps):
+                fn()
+            torch.cuda.synchronize()
+            done[f"{name}_N{N}"] = {"warm_launches": warm, "profiled_launches": reps,
+                                    "flops_per_launch": 2 * N**3}
+        del A, B, C
+    return done
 
 
 def profile_split_pass(em, torch, m: int = 512, reps: int = 20) -> dict:
