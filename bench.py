@@ -52,10 +52,17 @@ BF16_MFMA_PEAK_TFLOPS = 2516.6   # MI355X dense bf16 (no sparsity)
 EXACT_SPLIT_PEAK_TFLOPS = BF16_MFMA_PEAK_TFLOPS / 3
 
 
-def q8_kernel(m: int, k: int = 4096, n: int = 4096) -> tuple:
-    """(kernel name, compute peak in TFLOP/s) that automatic uses for int8 B
-    (row-major, unregistered): the GEMV up to 4 rows of small weights, the
-    exact-split kernel from 5 rows (split_bf16_preferred)."""
+def q8_kernel(m: int, k: int = 4096, n: int = 4096, registered: bool = False) -> tuple:
+    """(kernel name, compute peak in TFLOP/s) that automatic uses for int8 B.
+    Registered weights (em_q8_register, as DeviceQTensor does): one row runs
+    the strip-copy GEMV, 2 - 4 rows (k <= 4096) and 5 - 8 rows (k, n <= 4096)
+    the strip-copy MFMA kernel (decode_mfma_supported). Otherwise (and
+    unregistered): the GEMV up to 4 rows of small weights, the exact-split
+    kernel from 5 rows (split_bf16_preferred)."""
+    if registered and m == 1 and k <= 8192:
+        return "strip-copy GEMV (fp32 VALU)", FP32_MFMA_PEAK_TFLOPS / 2
+    if registered and 2 <= m <= 8 and k <= 4096 and k % 4 == 0 and (m <= 4 or n <= 4096):
+        return "strip-copy fp32 MFMA (v_mfma_f32_4x4x1_16b_f32)", FP32_MFMA_PEAK_TFLOPS
     w = k * n
     if m < 5 and not (m >= 3 and w >= 1 << 25) and not (m >= 2 and w >= 1 << 26):
         return "skinny GEMV (fp32 VALU)", FP32_MFMA_PEAK_TFLOPS / 2
@@ -1051,9 +1058,13 @@ def main() -> int:
     q_keep = None
     gemm_AB = None
     if not args.no_extra:
-        for m in (4, 8, 16, 32, 64):  # bench_cuda.cpp:112-144's decode rows
-            r, _ = gemv_case(em, torch, m, True, max(5, steps // 2), 2)
-            kname, peak = q8_kernel(m)
+        # bench_cuda.cpp:112-144's decode rows, over registered weights as
+        # the headline (what DeviceQTensor callers get), with the row-major
+        # (unregistered) call beside each.
+        for m in (4, 8, 16, 32, 64):
+            r, _ = gemv_case(em, torch, m, True, max(5, steps // 2), 2, register=True)
+            rr, _ = gemv_case(em, torch, m, True, max(5, steps // 2), 2)
+            kname, peak = q8_kernel(m, registered=True)
             t_mfma = r["flops_per_call"] / (peak * 1e12)
             t_hbm = r["bytes_per_call"] / (HBM_PEAK_GBS * 1e9)
             extra[f"int8_gemv_m{m}"] = {"us": round(r["us_per_call"], 3),
@@ -1061,7 +1072,9 @@ def main() -> int:
                                         "TFLOPS": round(r["flops_per_call"] / r["us_per_call"] / 1e6, 2),
                                         "kernel": kname, "compute_roof_TFLOPS": round(peak, 1),
                                         "bound": "mfma" if t_mfma > t_hbm else "hbm",
-                                        "pct_of_roofline": round(100 * max(t_mfma, t_hbm) * 1e6 / r["us_per_call"], 1)}
+                                        "pct_of_roofline": round(100 * max(t_mfma, t_hbm) * 1e6 / r["us_per_call"], 1),
+                                        "unregistered_rowmajor_us": round(rr["us_per_call"], 3),
+                                        "unregistered_kernel": q8_kernel(m)[0]}
         r, _ = gemv_case(em, torch, 1, False, max(5, steps // 2), 2)
         extra["fp32_gemv_m1"] = {"us": round(r["us_per_call"], 3), "GBps": round(r["GBps"], 1),
                                  "pct_of_hbm_peak": round(100 * r["GBps"] / HBM_PEAK_GBS, 1)}

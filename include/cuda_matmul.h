@@ -111,9 +111,9 @@ public:
             if (!t.scale.empty())
                 em_detail::check(
                     em_memcpy_h2d(scale_, t.scale.data(), t.scale.size() * sizeof(float)));
-            // The library's strip copy of the bytes (em_q8_register): one-row
-            // products over this matrix then run in one launch. The bytes are
-            // never written again, so the copy stays valid.
+            // The library's strip copy of the bytes (em_q8_register): products
+            // of up to 8 rows over this matrix then run in one launch. The
+            // bytes are never written again, so the copy stays valid.
             em_detail::check(em_q8_register(data_, rows_, cols_, EM_STREAM_PER_THREAD));
         } catch (...) {
             em_q8_unregister(data_);

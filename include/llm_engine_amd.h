@@ -111,36 +111,42 @@ int em_matmul_q8_noalloc(size_t m, size_t n, size_t k, const float* A, const int
  * The reference keeps int8 weights row-major (QTensor, tensor.h:23-28); the
  * entry points above take that layout. The strip layout is an opt-in copy for
  * decode-shaped products: n / 16 strips of 16 columns, strip j holding rows
- * 0 .. k - 1 of columns 16j .. 16j + 15 contiguously,
- *     packed[(j * k + r) * 16 + t] = B[r * n + 16 j + t],
+ * 0 .. k - 1 of columns 16j .. 16j + 15 contiguously in quads of four rows,
+ * each quad as four 16-byte units, unit c holding columns 4c .. 4c + 3 of the
+ * quad's four rows, row by row:
+ *     packed[(j * k + 4q) * 16 + 16c + 4t + u] = B[(4q + t) * n + 16j + 4c + u],
  * the same bytes reordered (scales unchanged). An m <= 8 product over it is
- * one launch with no split-K partials. Needs n % 16 == 0 and 16-byte aligned
- * buffers of k * n bytes. No counterpart in the reference. */
+ * one launch with no split-K partials. Needs n % 16 == 0, k % 4 == 0 and
+ * 16-byte aligned buffers of k * n bytes. No counterpart in the reference. */
 int em_pack_q8(size_t k, size_t n, const int8_t* B, int8_t* packed, void* stream);
 int em_unpack_q8(size_t k, size_t n, const int8_t* packed, int8_t* B, void* stream);
 /* Registers row-major int8 weights B (k x n, device memory) for em_matmul_q8:
  * the library keeps a strip-layout copy, packed from B's bytes on `stream`
- * (then drained), and em_matmul_q8 with EM_KERNEL_AUTOMATIC or
- * EM_KERNEL_SKINNY runs one-row products (m == 1, k <= 8192) over that copy
- * in one launch: same semantics, results within the same tolerance of the
- * row-major path, bit-identical across repeats. B's bytes must not change
- * while it is registered (register again after changing them); unregister
- * before freeing B. Registering again replaces the copy. Shapes the layout
- * cannot hold (n % 16 != 0, misaligned B) and EM_STRIP_COPY=0 in the
- * environment leave B unregistered (EM_OK). The C++ DeviceQTensor registers
- * its buffer on construction and unregisters it on destruction, so the
- * reference's callers (cuda_model.cu:112,167; bench_cuda.cpp:123,139) get
- * the one-launch product unchanged. No counterpart in the reference. */
+ * (then drained), and em_matmul_q8 runs decode-shaped products over that
+ * copy in one launch: one row (m == 1, k <= 8192) with EM_KERNEL_AUTOMATIC
+ * or EM_KERNEL_SKINNY, and, with EM_KERNEL_AUTOMATIC, 2 - 4 rows at
+ * k <= 4096 and 5 - 8 rows at k, n <= 4096 (A 16-byte aligned). Same
+ * semantics, results within the same tolerance of the row-major path,
+ * bit-identical across repeats. B's bytes must not change while it is
+ * registered (register again after changing them); unregister before
+ * freeing B. Registering again replaces the copy. Shapes the layout cannot
+ * hold (n % 16 != 0, k % 4 != 0, misaligned B) and EM_STRIP_COPY=0 in the
+ * environment leave B unregistered (EM_OK); EM_DECODE_MFMA=0 keeps 2 - 8
+ * rows on the row-major kernels. The C++ DeviceQTensor registers its buffer
+ * on construction and unregisters it on destruction, so the reference's
+ * callers (cuda_model.cu:112,167; bench_cuda.cpp:123,139) get the one-launch
+ * products unchanged. No counterpart in the reference. */
 int em_q8_register(const int8_t* B, size_t k, size_t n, void* stream);
 int em_q8_unregister(const int8_t* B);
 /* 1 if B has a strip copy of shape k x n, else 0. */
 int em_q8_registered(const int8_t* B, size_t k, size_t n);
 /* C = A x dequantize(B) (C += if accumulate; A replaced by rmsnorm(A) *
  * rms_weight when given), B in the strip layout: the semantics of
- * em_matmul_q8 for m <= 8 rows, in one launch, bit-identical across repeats.
- * EM_EINVAL for m > 8, n % 16 != 0, a misaligned B, more than 2^31
- * elements; m == 0 or n == 0 does nothing; k == 0 zeroes C unless
- * accumulating. */
+ * em_matmul_q8 for m <= 8 rows, in one launch, bit-identical across repeats
+ * (the same kernels and bits as a registered em_matmul_q8 call where that
+ * runs over the copy). EM_EINVAL for m > 8, n % 16 != 0, k % 4 != 0, a
+ * misaligned B, more than 2^31 elements; m == 0 or n == 0 does nothing;
+ * k == 0 zeroes C unless accumulating. */
 int em_matmul_q8_packed(size_t m, size_t n, size_t k, const float* A, const int8_t* packed,
                         const float* scale, float* C, int accumulate, const float* rms_weight,
                         void* stream);

@@ -54,10 +54,12 @@ def _run(cmd):
 # each rescale copies them out of and back into AGPRs (~300 moves per 128
 # MFMAs), so its MFMAs write VGPRs instead. gemm_mfma.hip: in the AGPR form
 # the one-workgroup-per-CU build of the fp32 GEMM loop moved accumulators
-# between AGPRs and VGPRs (80 moves per 256 MFMAs).
+# between AGPRs and VGPRs (80 moves per 256 MFMAs). decode_mfma.hip: its
+# accumulators are read by VALU reductions right after the loop.
 FILE_FLAGS = {
     "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "gemm_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "decode_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

@@ -72,6 +72,16 @@ const int8_t* strip_copy_of(const void* B, std::size_t k, std::size_t n) {
 // with m and the row-major kernels win.
 constexpr std::size_t kStripMaxK = 8192;
 
+// Decode batches (2 .. 16 rows) over registered weights: decode_mfma.hip.
+// EM_DECODE_MFMA=0 keeps them on the row-major kernels.
+bool decode_mfma_enabled() {
+    static const bool on = [] {
+        const char* v = std::getenv("EM_DECODE_MFMA");
+        return !(v && v[0] == '0');
+    }();
+    return on;
+}
+
 }  // namespace
 
 // The matmul entry points. `workspace` (em_matmul_q8_noalloc, with the
@@ -140,6 +150,14 @@ int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, co
             k <= kStripMaxK) {
             if (const int8_t* P = strip_copy_of(B, k, n)) {
                 run_gemv_packed(a, P);
+                hip_check(hipGetLastError(), "launch");
+                return EM_OK;
+            }
+        }
+        if (std::is_same<BT, int8_t>::value && automatic && m >= 2 && decode_mfma_enabled() &&
+            decode_mfma_supported(a)) {
+            if (const int8_t* P = strip_copy_of(B, k, n)) {
+                run_decode_mfma(a, P);
                 hip_check(hipGetLastError(), "launch");
                 return EM_OK;
             }
@@ -377,8 +395,9 @@ int em_dequantize_q8(size_t rows, size_t cols, const int8_t* q, const float* sca
 
 int em_pack_q8(size_t k, size_t n, const int8_t* B, int8_t* packed, void* stream) {
     if (too_many(k, n)) return fail(EM_EINVAL, "pack_q8: more than 2^31 elements");
-    if (n % 16) return fail(EM_EINVAL, "pack_q8: n must be a multiple of 16 (B is " +
-                                           std::to_string(k) + "x" + std::to_string(n) + ")");
+    if (n % 16 || k % 4)
+        return fail(EM_EINVAL, "pack_q8: n must be a multiple of 16 and k of 4 (B is " +
+                                   std::to_string(k) + "x" + std::to_string(n) + ")");
     if (k == 0 || n == 0) return EM_OK;
     if (!B || !packed) return fail(EM_EINVAL, "pack_q8: null pointer");
     if (reinterpret_cast<uintptr_t>(B) % 16 || reinterpret_cast<uintptr_t>(packed) % 16)
@@ -403,7 +422,7 @@ int em_q8_register(const int8_t* B, size_t k, size_t n, void* stream) {
         return !(v && v[0] == '0');
     }();
     // Shapes the strip layout cannot hold are left row-major.
-    if (!enabled || n % 16 || reinterpret_cast<uintptr_t>(B) % 16) return EM_OK;
+    if (!enabled || n % 16 || k % 4 || reinterpret_cast<uintptr_t>(B) % 16) return EM_OK;
     if (!em::device_present()) return fail(EM_ENODEV, "q8_register: no usable GPU");
     const hipStream_t s = static_cast<hipStream_t>(stream);
     try {
@@ -449,7 +468,8 @@ int em_q8_registered(const int8_t* B, size_t k, size_t n) {
 
 int em_unpack_q8(size_t k, size_t n, const int8_t* packed, int8_t* B, void* stream) {
     if (too_many(k, n)) return fail(EM_EINVAL, "unpack_q8: more than 2^31 elements");
-    if (n % 16) return fail(EM_EINVAL, "unpack_q8: n must be a multiple of 16");
+    if (n % 16 || k % 4)
+        return fail(EM_EINVAL, "unpack_q8: n must be a multiple of 16 and k of 4");
     if (k == 0 || n == 0) return EM_OK;
     if (!B || !packed) return fail(EM_EINVAL, "unpack_q8: null pointer");
     if (reinterpret_cast<uintptr_t>(B) % 16 || reinterpret_cast<uintptr_t>(packed) % 16)
@@ -473,8 +493,9 @@ int em_matmul_q8_packed(size_t m, size_t n, size_t k, const float* A, const int8
                                    em::shapes(m, n, k));
     if (too_many(m, k) || too_many(k, n) || too_many(m, n))
         return fail(EM_EINVAL, "matmul_q8_packed: more than 2^31 elements " + em::shapes(m, n, k));
-    if (n % 16)
-        return fail(EM_EINVAL, "matmul_q8_packed: n must be a multiple of 16 " + em::shapes(m, n, k));
+    if (n % 16 || k % 4)
+        return fail(EM_EINVAL, "matmul_q8_packed: n must be a multiple of 16 and k of 4 " +
+                                   em::shapes(m, n, k));
     if (m == 0 || n == 0) return EM_OK;
     if (!C) return fail(EM_EINVAL, "matmul_q8_packed: C is null " + em::shapes(m, n, k));
     if (k && (!A || !packed || !scale))
@@ -498,7 +519,10 @@ int em_matmul_q8_packed(size_t m, size_t n, size_t k, const float* A, const int8
             a.accumulate = accumulate != 0;
             a.rms_weight = rms_weight;
             a.stream = s;
-            em::run_gemv_packed(a, packed);
+            if (m >= 2 && em::decode_mfma_enabled() && em::decode_mfma_supported(a))
+                em::run_decode_mfma(a, packed);
+            else
+                em::run_gemv_packed(a, packed);
         }
         em::hip_check(hipGetLastError(), "launch");
     } catch (const std::exception& e) {

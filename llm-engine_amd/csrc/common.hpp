@@ -88,6 +88,76 @@ __device__ __forceinline__ float fold16(float x, float y) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// DPP move inside rows of 16 lanes: row_shl:8 (0x108) reads lane + 8,
+// row_shr:8 (0x118) lane - 8, row_shl:4 (0x104) lane + 4, row_shr:4 (0x114)
+// lane - 4. The control must be a constant of the instruction.
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// One step of lane_reduce16 over lane bit BIT (5, 4, 3 or 2). With N > 1
+// values the list is halved: a lane whose bit is clear keeps items
+// [0, N/2), a lane whose bit is set items [N/2, N), each summed with its
+// partner's copy of the same item. With one value left the partner's value
+// is added (both lanes form the same bits: a + b == b + a).
+template <int BIT, int N>
+__device__ __forceinline__ void lane_step(const float (&in)[N], float (&out)[N > 1 ? N / 2 : 1]) {
+    const bool hi = (threadIdx.x >> BIT) & 1;
+    constexpr int H = N > 1 ? N / 2 : 1;
+#pragma unroll
+    for (int t = 0; t < H; ++t) {
+        const float x = in[t], y = in[N > 1 ? t + H : t];
+        if constexpr (BIT == 5) {
+            out[t] = fold32(x, y);
+        } else if constexpr (BIT == 4) {
+            out[t] = fold16(x, y);
+        } else if constexpr (BIT == 3) {
+            const float lo_sum = x + dpp_row<0x108>(x), hi_sum = y + dpp_row<0x118>(y);
+            out[t] = hi ? hi_sum : lo_sum;
+        } else {
+            const float lo_sum = x + dpp_row<0x104>(x), hi_sum = y + dpp_row<0x114>(y);
+            out[t] = hi ? hi_sum : lo_sum;
+        }
+    }
+}
+
+// Sum of N values (a power of two) over the 16 lanes of a wave that share
+// lane & 3 (lane bits 5 .. 2), in a fixed pattern: reduce-scatter steps
+// while more than one value is left, then butterflies. Each lane ends with
+// max(N / 16, 1) sums; slot s holds list item lane_item<N>(lane, s).
+template <int N>
+__device__ __forceinline__ void lane_reduce16(const float (&v)[N], float (&out)[N >= 16 ? N / 16 : 1]) {
+    constexpr int N1 = N > 1 ? N / 2 : 1, N2 = N1 > 1 ? N1 / 2 : 1, N3 = N2 > 1 ? N2 / 2 : 1;
+    float a[N1], b[N2], c[N3];
+    lane_step<5, N>(v, a);
+    lane_step<4, N1>(a, b);
+    lane_step<3, N2>(b, c);
+    lane_step<2, N3>(c, out);
+}
+template <int N>
+__host__ __device__ constexpr int lane_item(int lane, int s) {
+    int t = s, count = N;
+    for (int bit = 5; bit >= 2; --bit) {
+        if (count > 1) {
+            count /= 2;
+            if ((lane >> bit) & 1) t += count;
+        }
+    }
+    return t;
+}
+// Whether this lane holds the one copy that is written out: lanes that
+// differ only in bits summed by butterflies hold the same sums.
+template <int N>
+__host__ __device__ constexpr bool lane_writes(int lane) {
+    int count = N;
+    for (int bit = 5; bit >= 2; --bit) {
+        if (count > 1) count /= 2;
+        else if ((lane >> bit) & 1) return false;
+    }
+    return true;
+}
+
 // Four int8 in one 32-bit word, widened to fp32. hipcc turns each into one
 // v_cvt_f32_i32 with an SDWA sign-extended byte select.
 __device__ __forceinline__ void widen4(uint32_t w, float* out) {

@@ -1,13 +1,16 @@
-// Decode-shaped products (m <= 8) over int8 weights held in the strip layout,
-// one launch per product: an explicit opt-in weight format behind the
-// boundary (the reference keeps QTensor row-major, tensor.h:23-28, and its
-// decode product is sgemm_skinny + sum_slices, cuda_matmul.cu:189-254,
-// 365-397).
+// Decode-shaped products over int8 weights held in the strip layout, one
+// launch per product: an explicit opt-in weight format behind the boundary
+// (the reference keeps QTensor row-major, tensor.h:23-28, and its decode
+// product is sgemm_skinny + sum_slices, cuda_matmul.cu:189-254, 365-397).
+// This file holds the layout and the one-row product (VALU); products of
+// 2 .. 8 rows run on MFMA over the same layout (decode_mfma.hip).
 //
-// Strip layout. A k x n int8 matrix (n % 16 == 0) is stored as n / 16 strips
-// of 16 columns; strip j holds rows 0 .. k - 1 of columns 16j .. 16j + 15,
-// 16 bytes a row, contiguously:
-//     packed[(j * k + r) * 16 + t] = B[r * n + 16 j + t].
+// Strip layout. A k x n int8 matrix (n % 16 == 0, k % 4 == 0) is stored as
+// n / 16 strips of 16 columns; strip j holds rows 0 .. k - 1 of columns
+// 16j .. 16j + 15 contiguously, in quads of four rows (64 bytes each), and a
+// quad in four 16-byte units, unit c holding columns 4c .. 4c + 3 of the
+// quad's rows, row by row:
+//     packed[(j * k + 4q) * 16 + 16c + 4t + u] = B[(4q + t) * n + 16j + 4c + u].
 // The bytes are the quantised bytes, only reordered, and the column scales
 // are unchanged.
 //
@@ -18,17 +21,22 @@
 // 4096^2 int8 matrix take to stream once a launch is running. In the strip
 // layout one workgroup reads all of k for its 16 columns as one contiguous
 // run, so no partial leaves the workgroup and the product is one launch.
+// The quads give every 16-byte load four rows of four columns: the four
+// lanes of a quad hold the same rows, which is what the 4x4 blocks of
+// v_mfma_f32_4x4x1_16b_f32 need (decode_mfma.hip), and a one-row lane reads
+// its four A values as one float4.
 //
-//  * Workgroup = one strip (256 threads). Lane t takes rows t, t + 256, ...:
-//    each load instruction of a wave reads 1 KiB of consecutive rows. All
-//    loads of a batch (L rows per lane) are in flight before any is used;
-//    with more than one batch the next batch loads while this one is summed.
+//  * Workgroup = one strip (256 threads). Thread t takes 16-byte units t,
+//    t + 256, ... of the strip: each load instruction of a wave reads 1 KiB
+//    of consecutive units. All loads of a batch (L units per lane) are in
+//    flight before any is used; with more than one batch the next batch
+//    loads while this one is summed.
 //  * int8 is widened in registers and summed unscaled; the column scale is
 //    applied once to the reduced sum.
-//  * The 64 lanes of a wave are reduced by a fixed reduce-scatter (16 values
-//    per lane -> one column per lane: lane swaps across halves and rows, DPP
-//    inside rows), the four waves in LDS in wave order. Every order is fixed,
-//    so repeated calls give the same bits.
+//  * A lane's four column sums are reduced over the 16 lanes holding the
+//    same columns by a fixed reduce-scatter (lane_reduce16), the waves in
+//    LDS in wave order. Every order is fixed, so repeated calls give the
+//    same bits.
 //  * A is staged in LDS per batch (float4 loads issued before the weights,
 //    so waiting for them does not wait for the weight stream).
 //  * With a norm weight, the workgroup forms the row's RMS scale from a pass
@@ -36,6 +44,7 @@
 //    normalises each A value as it uses it, as rmsnorm_rows does.
 #include <algorithm>
 #include <cstdlib>
+#include <string>
 
 #include "common.hpp"
 #include "internal.hpp"
@@ -55,83 +64,43 @@ struct PackedParams {
     int accumulate;
 };
 
-// Thread t of a 256-thread workgroup copies 16 bytes: strip j, row r with
-// j * k + r = global index, so the writes are contiguous.
+// Thread i writes 16-byte unit i of the packed matrix: strip j, quad q,
+// unit c with i = (j * k/4 + q) * 4 + c, from four 4-byte words of B (rows
+// 4q .. 4q + 3, columns 16j + 4c .. + 3). Threads walk q slowest, so
+// neighbours read neighbouring columns of the same rows.
 __global__ __launch_bounds__(kThreads) void pack_strips_kernel(int k, int n, const int8_t* B,
                                                                int8_t* P) {
-    const long long strips = n / kStrip;
-    const long long total = strips * k;
+    const long long strips = n / kStrip, quads = k / 4;
+    const long long total = strips * quads * 4;
     for (long long i = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x; i < total;
          i += static_cast<long long>(gridDim.x) * kThreads) {
-        const long long j = i / k, r = i - j * k;
-        const uint4 v = *reinterpret_cast<const uint4*>(B + r * n + j * kStrip);
-        *reinterpret_cast<uint4*>(P + i * kStrip) = v;
+        const long long q = i / (strips * 4), rest = i - q * strips * 4;
+        const long long j = rest / 4, c = rest % 4;
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(B + 4 * q * n + j * kStrip + 4 * c);
+        uint4 v;
+        v.x = src[0];
+        v.y = src[n / 4];
+        v.z = src[2 * (n / 4)];
+        v.w = src[3 * (n / 4)];
+        *reinterpret_cast<uint4*>(P + ((j * quads + q) * 4 + c) * 16) = v;
     }
 }
 
 __global__ __launch_bounds__(kThreads) void unpack_strips_kernel(int k, int n, const int8_t* P,
                                                                  int8_t* B) {
-    const long long strips = n / kStrip;
-    const long long total = strips * k;
+    const long long strips = n / kStrip, quads = k / 4;
+    const long long total = strips * quads * 4;
     for (long long i = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x; i < total;
          i += static_cast<long long>(gridDim.x) * kThreads) {
-        const long long j = i / k, r = i - j * k;
-        *reinterpret_cast<uint4*>(B + r * n + j * kStrip) =
-            *reinterpret_cast<const uint4*>(P + i * kStrip);
+        const long long q = i / (strips * 4), rest = i - q * strips * 4;
+        const long long j = rest / 4, c = rest % 4;
+        const uint4 v = *reinterpret_cast<const uint4*>(P + ((j * quads + q) * 4 + c) * 16);
+        uint32_t* dst = reinterpret_cast<uint32_t*>(B + 4 * q * n + j * kStrip + 4 * c);
+        dst[0] = v.x;
+        dst[n / 4] = v.y;
+        dst[2 * (n / 4)] = v.z;
+        dst[3 * (n / 4)] = v.w;
     }
-}
-
-// Sum over the 64 lanes, per column: on entry lane l holds 16 column sums
-// v[0..15]; on exit lane l holds the wave's total of column l >> 2 (the four
-// lanes of a group hold the same bits). Four halving steps, each adding a
-// lane's kept half to its partner's copy of the same half, then two full
-// steps:
-//   distance 32: v_permlane32_swap exchanges x's upper 32 lanes with y's
-//                lower 32, so x + y gives lanes 0-31 column i and lanes
-//                32-63 column i + 8 (x = v[i], y = v[i + 8]);
-//   distance 16: v_permlane16_swap exchanges x's odd rows of 16 with y's
-//                even rows, the same way;
-//   distance 8, 4: DPP row_shl / row_shr inside a row of 16, the lane's bit
-//                picking which half it keeps;
-//   distance 2, 1: DPP quad permutations (both lanes compute a + b in some
-//                order; the sum is the same bits either way).
-// Every value is added exactly once in a fixed place, so the result does not
-// depend on timing. No LDS is touched.
-__device__ __forceinline__ float dpp_f(float v, int ctrl) {
-    switch (ctrl) {  // the control must be a constant of the instruction
-        case 0x108: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x108, 0xf, 0xf, false));
-        case 0x118: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x118, 0xf, 0xf, false));
-        case 0x104: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x104, 0xf, 0xf, false));
-        case 0x114: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x114, 0xf, 0xf, false));
-        case 0xB1: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));
-        default: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));
-    }
-}
-
-__device__ __forceinline__ float wave_reduce_scatter16(float (&v)[16]) {
-    const int lane = threadIdx.x % kWave;
-    float a8[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) a8[i] = fold32(v[i], v[i + 8]);
-    float a4[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) a4[i] = fold16(a8[i], a8[i + 4]);
-    // DPP reads a lane that is switched off as zero, so both sides of each
-    // choice are formed by every lane (outside any branch), then selected.
-    const bool b3 = lane & 8, b2 = lane & 4;
-    float a2[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {  // row_shl:8 reads lane + 8, row_shr:8 lane - 8
-        const float keep_lo = a4[i] + dpp_f(a4[i], 0x108);
-        const float keep_hi = a4[i + 2] + dpp_f(a4[i + 2], 0x118);
-        a2[i] = b3 ? keep_hi : keep_lo;
-    }
-    const float keep_lo = a2[0] + dpp_f(a2[0], 0x104);
-    const float keep_hi = a2[1] + dpp_f(a2[1], 0x114);
-    float a1 = b2 ? keep_hi : keep_lo;
-    a1 += dpp_f(a1, 0xB1);  // quad_perm [1, 0, 3, 2]: lane ^ 1
-    a1 += dpp_f(a1, 0x4E);  // quad_perm [2, 3, 0, 1]: lane ^ 2
-    return a1;
 }
 
 // Sum over the workgroup's NW waves, every thread gets the result: wave
@@ -149,20 +118,23 @@ __device__ __forceinline__ float group_sum(float v, float* part) {
     return t;
 }
 
-// NT threads per workgroup (one strip), L rows per lane per batch.
-// VEC: k % 4 == 0 and A 16-byte aligned (A staged as float4). MULTI: k is
-// more than one batch (the next batch loads while this one is summed).
+// NT threads per workgroup (one strip), L units per lane per batch (a
+// batch covers NT * L rows). VEC: A 16-byte aligned (k % 4 == 0 always).
+// MULTI: k is more than one batch (the next batch loads while this one is
+// summed).
 template <int NT, int MM, int L, bool NORM, bool VEC, bool MULTI>
 __global__ __launch_bounds__(NT) void gemv_packed_kernel(PackedParams p) {
     constexpr int NW = NT / kWave;
     constexpr int RB = NT * L;              // rows of the strip per batch
     constexpr int NF = MM * RB / 4 / NT;    // A float4s per thread per batch
     static_assert(NF >= 1 && MM * RB % (4 * NT) == 0, "whole float4 slots per thread");
+    constexpr int NV = 4 * MM;              // column sums per lane: 4 columns x MM rows
+    constexpr int NO = NV >= 16 ? NV / 16 : 1;
     __shared__ float4 a_s4[MM * RB / 4];
     __shared__ float red[NW][MM][kStrip];
     __shared__ float part[NW];
-    const float* a_s = reinterpret_cast<const float*>(a_s4);
     const int tid = threadIdx.x;
+    const int c = tid & 3;  // the unit's column group
     const int strip = blockIdx.x;
     const int8_t* base = p.P + static_cast<size_t>(strip) * p.k * kStrip;
     const int batches = MULTI ? (p.k + RB - 1) / RB : 1;
@@ -206,40 +178,62 @@ __global__ __launch_bounds__(NT) void gemv_packed_kernel(PackedParams p) {
             a_s4[sl] = v;
         }
     };
-    // Weights of batch b: rows b * RB + tid + NT i (past k: row k - 1, whose
-    // A value is zero).
+    // Weights of batch b: units b * RB + tid + NT i of the strip (rows
+    // b * RB + NT i + (tid & ~3) .. + 3); past k the last quad's unit c,
+    // whose A values are zero.
     auto load_w = [&](int b, uint4 (&w)[L]) {
 #pragma unroll
         for (int i = 0; i < L; ++i) {
-            const int row = min(b * RB + tid + i * NT, p.k - 1);
-            w[i] = stream_load(reinterpret_cast<const uint4*>(base + static_cast<size_t>(row) * kStrip));
+            const int unit = min(b * RB + tid + i * NT, p.k - 4 + c);
+            w[i] = stream_load(reinterpret_cast<const uint4*>(base + static_cast<size_t>(unit) * kStrip));
         }
     };
 
-    float acc[MM][kStrip];
+    // One accumulator per (row of A, row of the quad, column) for one row of
+    // A, so a unit's 16 multiply-adds are independent; with more rows of A
+    // the quad's rows share one (the registers go to the rows).
+    constexpr int AT = MM == 1 ? 4 : 1;
+    float acc[MM][AT][4];
 #pragma unroll
     for (int r = 0; r < MM; ++r)
 #pragma unroll
-        for (int j = 0; j < kStrip; ++j) acc[r][j] = 0.0f;
+        for (int t = 0; t < AT; ++t)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[r][t][u] = 0.0f;
     auto fma_batch = [&](const uint4 (&w)[L], const float (&rs)[MM], int b) {
+        // One row of A: every A value of the batch read from LDS up front
+        // (16 bytes per unit), so no multiply-add waits on an LDS read.
+        float4 apre[MM == 1 ? L : 1];
+        if constexpr (MM == 1) {
+#pragma unroll
+            for (int i = 0; i < L; ++i) apre[i] = a_s4[(i * NT + (tid & ~3)) / 4];
+        }
 #pragma unroll
         for (int i = 0; i < L; ++i) {
-            float bv[kStrip];
-            widen4(w[i].x, bv);
-            widen4(w[i].y, bv + 4);
-            widen4(w[i].z, bv + 8);
-            widen4(w[i].w, bv + 12);
-            const int pl = tid + i * NT;
+            float bv[4][4];  // [row t of the quad][column 4c + u]
+            widen4(w[i].x, bv[0]);
+            widen4(w[i].y, bv[1]);
+            widen4(w[i].z, bv[2]);
+            widen4(w[i].w, bv[3]);
+            const int pl = i * NT + (tid & ~3);  // the quad's first row in the batch
 #pragma unroll
             for (int r = 0; r < MM; ++r) {
-                float a = a_s[r * RB + pl];
+                float4 a4 = MM == 1 ? apre[i % (MM == 1 ? L : 1)] : a_s4[(r * RB + pl) / 4];
+                float a[4] = {a4.x, a4.y, a4.z, a4.w};
                 if constexpr (NORM) {
-                    const int row = b * RB + pl;
-                    a = row < p.k ? a * rs[r] * p.rms_weight[row] : 0.0f;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const int row = b * RB + pl + t;
+                        a[t] = row < p.k ? a[t] * rs[r] * p.rms_weight[row] : 0.0f;
+                    }
                 }
 #pragma unroll
-                for (int j = 0; j < kStrip; ++j) acc[r][j] = fmaf(a, bv[j], acc[r][j]);
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        acc[r][t % AT][u] = fmaf(a[t], bv[t][u], acc[r][t % AT][u]);
             }
+            if constexpr (MM > 1) __builtin_amdgcn_sched_barrier(0);
         }
     };
 
@@ -296,11 +290,26 @@ __global__ __launch_bounds__(NT) void gemv_packed_kernel(PackedParams p) {
         }
     }
 
+    // Item u * MM + r is column 4c + u of row r; lane_reduce16 sums it over
+    // the wave's 16 lanes with the same c.
     const int wave = tid / kWave, lane = tid % kWave;
+    float v[NV], o[NO];
 #pragma unroll
-    for (int r = 0; r < MM; ++r) {
-        const float s = wave_reduce_scatter16(acc[r]);
-        if ((lane & 3) == 0) red[wave][r][lane >> 2] = s;
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int r = 0; r < MM; ++r) {
+            float x = acc[r][0][u];
+#pragma unroll
+            for (int t = 1; t < AT; ++t) x += acc[r][t][u];
+            v[u * MM + r] = x;
+        }
+    lane_reduce16<NV>(v, o);
+    if (lane_writes<NV>(lane)) {
+#pragma unroll
+        for (int s = 0; s < NO; ++s) {
+            const int t = lane_item<NV>(lane, s);
+            red[wave][t % MM][4 * c + t / MM] = o[s];
+        }
     }
     __syncthreads();
     if (eout) {

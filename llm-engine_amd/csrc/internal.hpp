@@ -195,6 +195,10 @@ void run_pack_strips(int k, int n, const int8_t* B, int8_t* P, hipStream_t strea
 void run_unpack_strips(int k, int n, const int8_t* P, int8_t* B, hipStream_t stream);
 // C (+)= rmsnorm?(A) x B for m <= 8 rows, B in the strip layout, one launch.
 void run_gemv_packed(const MatmulArgs& a, const int8_t* packed);
+// 2 .. 8 rows over a strip-layout copy, fp32 MFMA, one launch
+// (decode_mfma.hip): n % 16 == 0, k % 4 == 0, k <= 4096, A 16-byte aligned.
+bool decode_mfma_supported(const MatmulArgs& a);
+void run_decode_mfma(const MatmulArgs& a, const int8_t* packed);
 
 void run_quantize_q8(int rows, int cols, const float* B, int8_t* q, float* scale,
                      hipStream_t stream);

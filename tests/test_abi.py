@@ -173,6 +173,8 @@ def test_packed_layout_checks_before_the_gpu():
     L = em.lib()
     assert L.em_pack_q8(4, 17, 16, 16, None) == em.EM_EINVAL
     assert b"multiple of 16" in L.em_last_error()
+    assert L.em_pack_q8(5, 16, 16, 16, None) == em.EM_EINVAL
+    assert b"k of 4" in L.em_last_error()
     assert L.em_pack_q8(0, 16, None, None, None) == em.EM_OK
     assert L.em_pack_q8(4, 16, None, 16, None) == em.EM_EINVAL
     assert L.em_pack_q8(4, 16, 8, 16, None) == em.EM_EINVAL
@@ -182,6 +184,8 @@ def test_packed_layout_checks_before_the_gpu():
     assert e.code == em.EM_EINVAL and "at most 8 rows" in str(e) and "9x4" in str(e)
     e = err(lambda: em._check(L.em_matmul_q8_packed(1, 20, 4, 16, 16, 16, 16, 0, None, None)))
     assert e.code == em.EM_EINVAL and "multiple of 16" in str(e)
+    e = err(lambda: em._check(L.em_matmul_q8_packed(1, 16, 5, 16, 16, 16, 16, 0, None, None)))
+    assert e.code == em.EM_EINVAL and "k of 4" in str(e)
     e = err(lambda: em._check(L.em_matmul_q8_packed(1, 16, 4, 16, 8, 16, 16, 0, None, None)))
     assert e.code == em.EM_EINVAL and "aligned" in str(e)
     e = err(lambda: em._check(L.em_matmul_q8_packed(1, 16, 4, 16, 16, None, 16, 0, None, None)))

@@ -31,12 +31,30 @@ def host(t):
 
 
 def strips(q):
-    """The layout by its definition: packed[(j * k + r) * 16 + t] = B[r, 16 j + t]."""
+    """The layout by its definition, written as loops over its indices:
+    packed[(j * k + 4 qd) * 16 + 16 c + 4 t + u] = B[4 qd + t, 16 j + 4 c + u]."""
     k, n = q.shape
-    return np.ascontiguousarray(q.reshape(k, n // 16, 16).transpose(1, 0, 2)).reshape(-1)
+    out = np.empty(k * n, dtype=q.dtype)
+    j, qd, c, t, u = np.meshgrid(np.arange(n // 16), np.arange(k // 4), np.arange(4), np.arange(4),
+                                 np.arange(4), indexing="ij")
+    out[(j * k + 4 * qd) * 16 + 16 * c + 4 * t + u] = q[4 * qd + t, 16 * j + 4 * c + u]
+    return out
 
 
-@pytest.mark.parametrize("shape", [(1, 16), (3, 32), (288, 864), (17, 4096), (4096, 4096),
+def test_strips_reference_is_a_permutation():
+    # The definition above, checked on a matrix of distinct values: every
+    # byte lands once, and a quad's unit c holds rows 4q..4q+3 of columns
+    # 4c..4c+3, row by row.
+    k, n = 8, 32
+    q = np.arange(k * n, dtype=np.int32).reshape(k, n)
+    got = strips(q)
+    assert np.array_equal(np.sort(got), np.arange(k * n))
+    # strip 1, quad 1, unit 2: rows 4..7 of columns 16 + 8 .. 16 + 11.
+    unit = got[(1 * k + 4) * 16 + 32:(1 * k + 4) * 16 + 48].reshape(4, 4)
+    assert np.array_equal(unit, q[4:8, 24:28])
+
+
+@pytest.mark.parametrize("shape", [(4, 16), (12, 32), (288, 864), (20, 4096), (4096, 4096),
                                    (11008, 64)], ids=lambda s: "x".join(map(str, s)))
 def test_pack_layout_and_round_trip(shape):
     k, n = shape
@@ -47,13 +65,24 @@ def test_pack_layout_and_round_trip(shape):
     assert np.array_equal(host(em.unpack_q8(packed, k, n)), q)
 
 
+def test_pack_rejects_k_not_a_multiple_of_4():
+    q = torch.zeros((17, 32), dtype=torch.int8, device="cuda")
+    with pytest.raises(em.EngineError, match="multiple of 16 and k of 4"):
+        em.pack_q8(q)
+    A = torch.zeros((1, 17), device="cuda")
+    with pytest.raises(em.EngineError, match="multiple of 16 and k of 4"):
+        em.matmul_packed(A, torch.zeros((17 * 32,), dtype=torch.int8, device="cuda"), 32,
+                         torch.ones((32,), device="cuda"))
+
+
 # (m, k, n): decode rows 1..8 against the stories15M and Llama-7B-shaped
-# projections, a k that needs several 4096-row batches (11008, 8193), and
-# k below one batch or not a multiple of 256.
+# projections, a k that needs several 4096-row batches (11008, 8196), k
+# below one batch or not a multiple of 256, and k past the MFMA kernel's
+# 4096 at 2 .. 8 rows (4100, 11008: the VALU kernel).
 SHAPES = [(1, 288, 864), (1, 288, 32000), (1, 768, 288), (1, 4096, 4096), (1, 11008, 4096),
-          (1, 8193, 64), (1, 1, 16), (1, 17, 48), (2, 300, 1536), (3, 4096, 272),
-          (4, 4097, 32), (5, 513, 2048), (8, 1000, 4096), (8, 11008, 64), (6, 20, 16),
-          (7, 2, 160)]
+          (1, 8196, 64), (1, 4, 16), (1, 20, 48), (2, 300, 1536), (3, 4096, 272),
+          (4, 4100, 32), (5, 516, 2048), (8, 1000, 4096), (8, 11008, 64), (6, 20, 16),
+          (7, 4, 160), (2, 4096, 4096), (4, 4096, 11008), (8, 4096, 4096), (5, 288, 32000)]
 
 
 def check(got, want, A, Bf, k, factor=1.0, C0=None):
@@ -133,7 +162,7 @@ def test_packed_graph_replay_matches_eager():
 
 # ---- registered weights: em_matmul_q8 over the strip copy -------------------
 
-REG_SHAPES = [(288, 864), (4096, 4096), (8192, 64), (768, 288), (288, 32000), (17, 48)]
+REG_SHAPES = [(288, 864), (4096, 4096), (8192, 64), (768, 288), (288, 32000), (20, 48)]
 
 
 @pytest.mark.parametrize("kernel", ["automatic", "skinny"])
@@ -168,29 +197,75 @@ def test_registered_one_row_against_oracle(shape, fusion, kernel):
     check(got, want, An, orc.dequantize(q, s), k, 2.0 if (acc or rms) else 1.0, C0)
 
 
+@pytest.mark.parametrize("fusion", ["plain", "acc", "rms", "rms_acc"])
+@pytest.mark.parametrize("shape", [(2, 288, 864), (4, 4096, 4096), (8, 4096, 11008), (3, 768, 288),
+                                   (6, 4096, 32000), (7, 20, 48), (5, 11008, 64), (8, 4096, 4096),
+                                   (4, 4096, 32000), (2, 1000, 2048)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_registered_decode_rows_against_oracle(shape, fusion):
+    # 2 .. 8 rows with automatic over registered weights: the MFMA kernel
+    # over the strip copy where it takes the shape (k <= 4096; 5 .. 8 rows
+    # only up to n = 4096), the row-major kernels otherwise; bit-identical
+    # on repeat, and the same bits as em_matmul_q8_packed where both run the
+    # MFMA kernel.
+    m, k, n = shape
+    A = inputs.uniform((m, k), -1.0, 1.0, 56)
+    q, s = orc.quantize_q8(inputs.normal((k, n), 0.02, 57))
+    acc = "acc" in fusion
+    rms = "rms" in fusion
+    C0 = inputs.uniform((m, n), -1.0, 1.0, 58) if acc else None
+    w = inputs.uniform((k,), 0.5, 1.5, 59) if rms else None
+    qd, sd = dev(q), dev(s)
+    wd = dev(w) if rms else None
+    em.register_q8(qd)
+    try:
+        outs = []
+        for _ in range(2):
+            C = dev(C0) if acc else torch.empty((m, n), device="cuda")
+            em.matmul(dev(A), qd, C, scale=sd, accumulate=acc, rms_weight=wd)
+            outs.append(host(C))
+        assert np.array_equal(outs[0], outs[1])
+        if k <= 4096 and (m <= 4 or n <= 4096):
+            # Both entry points run the MFMA kernel here.
+            C2 = dev(C0) if acc else torch.empty((m, n), device="cuda")
+            em.matmul_packed(dev(A), em.pack_q8(qd), n, sd, C2, accumulate=acc, rms_weight=wd)
+            assert np.array_equal(outs[0], host(C2))
+    finally:
+        em.unregister_q8(qd)
+    want = orc.matmul_fused(A, Bq=q, scale=s, w=w, C0=C0)
+    An = orc.rmsnorm(A, w) if rms else A
+    check(outs[0], want, An, orc.dequantize(q, s), k, 2.0 if (acc or rms) else 1.0, C0)
+
+
 def test_registered_weights_leave_other_calls_row_major():
-    # More than one row, an explicit MFMA kernel, k past the strip cut and an
+    # Explicit kernels, more than 8 rows, k past the strip cut and an
     # unregistered B all run the row-major kernels: the same bits as before
-    # registering.
+    # registering. One row and (automatic) 2 .. 8 rows run over the strip
+    # copy: the same bits as em_matmul_q8_packed, within the tolerance of the
+    # row-major path.
     k, n = 4096, 512
     q, s = em.quantize_q8(dev(inputs.normal((k, n), 0.02, 61)))
     A1 = dev(inputs.normal((1, k), 1.0, 62))
     A4 = dev(inputs.normal((4, k), 1.0, 63))
-    before = {name: host(em.matmul(A, q, scale=s, kernel=kern)).copy()
-              for name, A, kern in (("m4", A4, "automatic"), ("tiled", A1, "tiled"),
-                                    ("naive", A1, "naive"))}
-    row1 = host(em.matmul(A1, q, scale=s)).copy()
+    A12 = dev(inputs.normal((12, k), 1.0, 66))
+    same = (("m4 skinny", A4, "skinny"), ("m12", A12, "automatic"), ("tiled", A1, "tiled"),
+            ("naive", A1, "naive"))
+    before = {name: host(em.matmul(A, q, scale=s, kernel=kern)).copy() for name, A, kern in same}
+    row = {m: host(em.matmul(A, q, scale=s)).copy() for m, A in ((1, A1), (4, A4))}
     em.register_q8(q)
     try:
-        for name, A, kern in (("m4", A4, "automatic"), ("tiled", A1, "tiled"),
-                              ("naive", A1, "naive")):
+        for name, A, kern in same:
             assert np.array_equal(host(em.matmul(A, q, scale=s, kernel=kern)), before[name])
-        reg1 = host(em.matmul(A1, q, scale=s)).copy()
+        reg = {m: host(em.matmul(A, q, scale=s)).copy() for m, A in ((1, A1), (4, A4))}
+        P = em.pack_q8(q)
+        for m, A in ((1, A1), (4, A4)):
+            assert np.array_equal(reg[m], host(em.matmul_packed(A, P, n, s)))
     finally:
         em.unregister_q8(q)
-    assert np.array_equal(host(em.matmul(A1, q, scale=s)), row1)
-    bound = orc.abs_bound(host(A1), orc.dequantize(host(q), host(s)))
-    assert np.all(np.abs(reg1.astype(np.float64) - row1) <= 1e-4 * bound)
+    for m, A in ((1, A1), (4, A4)):
+        assert np.array_equal(host(em.matmul(A, q, scale=s)), row[m])
+        bound = orc.abs_bound(host(A), orc.dequantize(host(q), host(s)))
+        assert np.all(np.abs(reg[m].astype(np.float64) - row[m]) <= 1e-4 * bound)
     # k = 8193: past the strip cut, registered or not the row-major path.
     q2, s2 = em.quantize_q8(dev(inputs.normal((8193, 64), 0.02, 64)))
     A2 = dev(inputs.normal((1, 8193), 1.0, 65))
