@@ -61,7 +61,8 @@ def q8_kernel(m: int, k: int = 4096, n: int = 4096, registered: bool = False) ->
     kernel from 5 rows (split_bf16_preferred)."""
     if registered and m == 1 and k <= 8192:
         return "strip-copy GEMV (fp32 VALU)", FP32_MFMA_PEAK_TFLOPS / 2
-    if registered and 2 <= m <= 8 and k <= 4096 and k % 4 == 0 and (m <= 4 or n <= 4096):
+    if registered and 2 <= m <= 8 and k <= 4096 and k % 4 == 0 and (
+            m <= 2 or (m <= 4 and n <= 24576) or n <= 4096):
         return "strip-copy fp32 MFMA (v_mfma_f32_4x4x1_16b_f32)", FP32_MFMA_PEAK_TFLOPS
     w = k * n
     if m < 5 and not (m >= 3 and w >= 1 << 25) and not (m >= 2 and w >= 1 << 26):

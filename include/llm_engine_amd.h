@@ -124,8 +124,9 @@ int em_unpack_q8(size_t k, size_t n, const int8_t* packed, int8_t* B, void* stre
  * the library keeps a strip-layout copy, packed from B's bytes on `stream`
  * (then drained), and em_matmul_q8 runs decode-shaped products over that
  * copy in one launch: one row (m == 1, k <= 8192) with EM_KERNEL_AUTOMATIC
- * or EM_KERNEL_SKINNY, and, with EM_KERNEL_AUTOMATIC, 2 - 4 rows at
- * k <= 4096 and 5 - 8 rows at k, n <= 4096 (A 16-byte aligned). Same
+ * or EM_KERNEL_SKINNY, and, with EM_KERNEL_AUTOMATIC, 2 - 8 rows at
+ * k <= 4096 (3 - 4 rows up to n = 24576, 5 - 8 up to n = 4096; A 16-byte
+ * aligned). Same
  * semantics, results within the same tolerance of the row-major path,
  * bit-identical across repeats. B's bytes must not change while it is
  * registered (register again after changing them); unregister before

@@ -278,17 +278,22 @@ void launch_decode_threads(const DecodeParams& p, hipStream_t s) {
 }  // namespace
 
 // Where the kernel wins against the row-major products (registered 4096 x n
-// weights, per call): 2 - 4 rows at n = 4096 / 11008 / 32000: 5.5 - 6.3 /
-// 11.4 - 12.2 / 25.0 - 27.4 us against 7.4 - 8.7 / 12.9 - 15.1 / 26.4 -
-// 27.0; 5 - 8 rows only at n = 4096 (8.1 against 9.7 us), since every
-// workgroup reads all of A: with wider B the workgroups outnumber the CUs
-// (11008: 19.6 against 15.4 us). k is at most 4096 (all loads of a lane in
-// flight at once).
+// weights, per call, us):
+//   n        4096       11008        12288        22016        32000
+//   m = 2    5.5 / 7.4  11.6 / 12.9  11.8 / 12.8  19.3 / 22.6  26.1 / 26.8
+//   m = 4    6.3 / 8.7  12.5 / 15.0  13.5 / 16.0  21.6 / 22.9  29.0 / 27.1
+//   m = 8    8.1 / 9.7  20.5 / 15.5  21.7 / 16.4  38.1 / 23.3  50.3 / 27.4
+// So 2 rows at any width, 3 - 4 up to n = 24576, 5 - 8 only up to 4096:
+// every workgroup reads all of A, and wider B means more workgroups than
+// CUs. (Fetching A once for several strips per workgroup, 512 threads,
+// was slower at every one of these shapes: 4096 x 22016 at m = 4, 37.8
+// against 21.6 us.) k is at most 4096 (all loads of a lane in flight at
+// once).
 bool decode_mfma_supported(const MatmulArgs& a) {
     if (a.m < 2 || a.m > 8 || a.n % kStrip != 0 || a.k % 4 != 0 || a.k <= 0 ||
         a.k > kDecodeMaxQuads * 4 || reinterpret_cast<uintptr_t>(a.A) % 16 != 0)
         return false;
-    return a.m <= 4 || a.n <= 4096;
+    return a.m <= 2 || (a.m <= 4 && a.n <= 24576) || a.n <= 4096;
 }
 
 void run_decode_mfma(const MatmulArgs& a, const int8_t* packed) {

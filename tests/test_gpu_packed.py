@@ -204,10 +204,10 @@ def test_registered_one_row_against_oracle(shape, fusion, kernel):
                          ids=lambda s: "x".join(map(str, s)))
 def test_registered_decode_rows_against_oracle(shape, fusion):
     # 2 .. 8 rows with automatic over registered weights: the MFMA kernel
-    # over the strip copy where it takes the shape (k <= 4096; 5 .. 8 rows
-    # only up to n = 4096), the row-major kernels otherwise; bit-identical
-    # on repeat, and the same bits as em_matmul_q8_packed where both run the
-    # MFMA kernel.
+    # over the strip copy where it takes the shape (k <= 4096; 3 .. 4 rows up
+    # to n = 24576, 5 .. 8 up to 4096), the row-major kernels otherwise;
+    # bit-identical on repeat, and the same bits as em_matmul_q8_packed where
+    # both run the MFMA kernel.
     m, k, n = shape
     A = inputs.uniform((m, k), -1.0, 1.0, 56)
     q, s = orc.quantize_q8(inputs.normal((k, n), 0.02, 57))
@@ -225,7 +225,7 @@ def test_registered_decode_rows_against_oracle(shape, fusion):
             em.matmul(dev(A), qd, C, scale=sd, accumulate=acc, rms_weight=wd)
             outs.append(host(C))
         assert np.array_equal(outs[0], outs[1])
-        if k <= 4096 and (m <= 4 or n <= 4096):
+        if k <= 4096 and (m <= 2 or (m <= 4 and n <= 24576) or n <= 4096):
             # Both entry points run the MFMA kernel here.
             C2 = dev(C0) if acc else torch.empty((m, n), device="cuda")
             em.matmul_packed(dev(A), em.pack_q8(qd), n, sd, C2, accumulate=acc, rms_weight=wd)
