@@ -526,7 +526,7 @@ def profile_pass(em, torch, sweeps: int = 2) -> dict:
     a second buffer: that many bytes read and as many written, each once), the
     yardstick the HBM byte counters are scaled by; then the headline product
     (int8 m = 1, 4096^2) over the rotating pool, `sweeps` times with the pool
-    registered (the bench's value: gemv_packed_kernel), then `sweeps` times
+    registered (the bench's value: gemv_row_kernel), then `sweeps` times
     unregistered (row-major: gemv_kernel + reduce_slices)."""
     src = torch.randn(CALIBRATION_BYTES // 4, device="cuda")
     dst = torch.empty_like(src)
@@ -1038,7 +1038,7 @@ def main() -> int:
                      "traffic": traffic["hbm_bytes_per_call"] if traffic else None,
                      "traffic_note": (traffic["note"] if traffic else
                                       "no counter summary in profiles/"),
-                     "kernel": "gemv_packed_kernel<256,1,16> (one em_matmul_q8 call over a "
+                     "kernel": "gemv_row_kernel<512,8> (one em_matmul_q8 call over a "
                                "registered matrix: one launch, no split-K partials)",
                      "avg_launch_us": round(avg_launch_s * 1e6, 3),
                      "bytes_per_launch": head["bytes_per_call"],

@@ -2,8 +2,11 @@
 // launch per product: an explicit opt-in weight format behind the boundary
 // (the reference keeps QTensor row-major, tensor.h:23-28, and its decode
 // product is sgemm_skinny + sum_slices, cuda_matmul.cu:189-254, 365-397).
-// This file holds the layout and the one-row product (VALU); products of
-// 2 .. 8 rows run on MFMA over the same layout (decode_mfma.hip).
+// This file holds the layout and the VALU products over it: one row of A
+// up to k = 8192 in gemv_row_kernel (A loaded beside each weight unit),
+// and in gemv_packed_kernel (A staged in LDS per batch) deeper k, A not
+// 16-byte aligned, and the 2 .. 8 row shapes that the MFMA kernel over the
+// same layout (decode_mfma.hip) does not take.
 //
 // Strip layout. A k x n int8 matrix (n % 16 == 0, k % 4 == 0) is stored as
 // n / 16 strips of 16 columns; strip j holds rows 0 .. k - 1 of columns
@@ -26,25 +29,30 @@
 // v_mfma_f32_4x4x1_16b_f32 need (decode_mfma.hip), and a one-row lane reads
 // its four A values as one float4.
 //
-//  * Workgroup = one strip (256 threads). Thread t takes 16-byte units t,
-//    t + 256, ... of the strip: each load instruction of a wave reads 1 KiB
-//    of consecutive units. All loads of a batch (L units per lane) are in
-//    flight before any is used; with more than one batch the next batch
-//    loads while this one is summed.
+//  * Workgroup = one strip (256 or 512 threads). Thread t takes 16-byte
+//    units t, t + NT, ... of the strip: each load instruction of a wave
+//    reads 1 KiB of consecutive units. All loads of a batch (L units per
+//    lane) are in flight before any is used; with more than one batch the
+//    next batch loads while this one is summed.
 //  * int8 is widened in registers and summed unscaled; the column scale is
 //    applied once to the reduced sum.
 //  * A lane's four column sums are reduced over the 16 lanes holding the
 //    same columns by a fixed reduce-scatter (lane_reduce16), the waves in
 //    LDS in wave order. Every order is fixed, so repeated calls give the
 //    same bits.
-//  * A is staged in LDS per batch (float4 loads issued before the weights,
-//    so waiting for them does not wait for the weight stream).
-//  * With a norm weight, the workgroup forms the row's RMS scale from a pass
-//    over A (fixed order) while its first weights are in flight, and
-//    normalises each A value as it uses it, as rmsnorm_rows does.
+//  * gemv_row_kernel: each unit comes with its own float4 of A, loaded just
+//    before it; a fused norm weight is loaded the same way and the row's RMS
+//    scale, from sums of squares formed on the way, multiplies each output.
+//  * gemv_packed_kernel: A is staged in LDS per batch (float4 loads issued
+//    before the weights, so waiting for them does not wait for the weight
+//    stream). With a norm weight, the workgroup forms the row's RMS scale
+//    from a pass over A (fixed order) while its first weights are in
+//    flight, and normalises each A value as it uses it, as rmsnorm_rows
+//    does.
 #include <algorithm>
 #include <cstdlib>
 #include <string>
+#include <type_traits>
 
 #include "common.hpp"
 #include "internal.hpp"
@@ -321,6 +329,106 @@ __global__ __launch_bounds__(NT) void gemv_packed_kernel(PackedParams p) {
     }
 }
 
+// One row of A, all of k in one pass, nothing staged in LDS: unit i of a
+// lane (u = tid + i * NT) is loaded together with its own float4 of A (the
+// quad's rows u & ~3 .. + 3), issued just before the unit's weights. A
+// lane's first multiply-adds then wait for one A vector and one weight unit
+// instead of all of A and a barrier. (With A staged in LDS first, the wait
+// for A ended 1.4-1.8 us into a 3.6 us kernel at 4096^2, when most of the
+// weights had arrived, so the widening and multiply-adds ran after the
+// stream instead of beside it.) Units past k (TAIL) read the last quad's
+// unit c again with A zeroed. With a norm weight, the weight is loaded
+// beside A and multiplied in; the row's sum of squares is formed on the
+// way (counted from the c == 0 lanes, which between them hold each A value
+// once) and its RMS scale multiplies each reduced sum once.
+template <int NT, int L, bool NORM, bool TAIL>
+__global__ __launch_bounds__(NT) void gemv_row_kernel(PackedParams p) {
+    constexpr int NW = NT / kWave;
+    __shared__ float red[NW][kStrip + 1];
+    const int tid = threadIdx.x;
+    const int c = tid & 3;
+    const int strip = blockIdx.x;
+    const int8_t* base = p.P + static_cast<size_t>(strip) * p.k * kStrip;
+    float4 av[L];
+    float4 nv[NORM ? L : 1];
+    uint4 w[L];
+#pragma unroll
+    for (int i = 0; i < L; ++i) {
+        const int u = tid + i * NT;
+        const int uc = TAIL ? min(u, p.k - 4 + c) : u;
+        av[i] = *reinterpret_cast<const float4*>(p.A + (uc & ~3));
+        if constexpr (NORM) nv[i] = *reinterpret_cast<const float4*>(p.rms_weight + (uc & ~3));
+        w[i] = stream_load(reinterpret_cast<const uint4*>(base + static_cast<size_t>(uc) * kStrip));
+    }
+    // The epilogue's scale (and prior C) behind the weights, waited for at
+    // the end.
+    __builtin_amdgcn_sched_barrier(0);
+    const int ec = strip * kStrip + tid % kStrip;
+    const float esc = p.scale[ec];
+    const float eprior = p.accumulate ? p.C[ec] : 0.0f;
+    __builtin_amdgcn_sched_barrier(0);
+
+    float acc[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[t][u] = 0.0f;
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < L; ++i) {
+        float a[4] = {av[i].x, av[i].y, av[i].z, av[i].w};
+        if constexpr (TAIL) {
+            const bool in = tid + i * NT < p.k;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) a[t] = in ? a[t] : 0.0f;
+        }
+        if constexpr (NORM) {
+            const float g[4] = {nv[i].x, nv[i].y, nv[i].z, nv[i].w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                ss = fmaf(a[t], a[t], ss);
+                a[t] *= g[t];
+            }
+        }
+        float bv[4][4];  // [row t of the quad][column 4c + u]
+        widen4(w[i].x, bv[0]);
+        widen4(w[i].y, bv[1]);
+        widen4(w[i].z, bv[2]);
+        widen4(w[i].w, bv[3]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[t][u] = fmaf(a[t], bv[t][u], acc[t][u]);
+    }
+
+    // Column 4c + u summed over the quad's rows, then over the wave's 16
+    // lanes with the same c (lane_reduce16), then over the waves in order.
+    const int wave = tid / kWave, lane = tid % kWave;
+    float v[4], o[1];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = ((acc[0][u] + acc[1][u]) + acc[2][u]) + acc[3][u];
+    lane_reduce16<4>(v, o);
+    if (lane_writes<4>(lane)) red[wave][4 * c + lane_item<4>(lane, 0)] = o[0];
+    if constexpr (NORM) {
+        const float sw = wave_sum(c == 0 ? ss : 0.0f);
+        if (lane == 0) red[wave][kStrip] = sw;
+    }
+    __syncthreads();
+    if (tid < kStrip) {
+        float total = red[0][tid];
+#pragma unroll
+        for (int w2 = 1; w2 < NW; ++w2) total += red[w2][tid];
+        if constexpr (NORM) {
+            float sq = red[0][kStrip];
+#pragma unroll
+            for (int w2 = 1; w2 < NW; ++w2) sq += red[w2][kStrip];
+            total *= 1.0f / sqrtf(sq / static_cast<float>(p.k) + kRmsEps);
+        }
+        total *= esc;
+        p.C[ec] = p.accumulate ? eprior + total : total;
+    }
+}
+
 // Threads per workgroup: 256 by default; EM_PACKED_THREADS (256, 512 or
 // 1024) overrides it for tuning sweeps.
 int packed_threads() {
@@ -368,8 +476,67 @@ int packed_depth(int nt, int k, int lmax) {
 // may also run 512 or 1024 threads per strip, with 8192 / NT rows per lane
 // at most (the same rows per batch, the register budget per lane shrinking
 // with the waves per SIMD).
+// gemv_row_kernel at NT threads: the shallowest L (4 .. LMAX) whose NT x L
+// units hold all of k; false when k is deeper than that.
+template <int NT, bool NORM>
+bool launch_row(const PackedParams& p, hipStream_t s) {
+    constexpr int LMAX = NT == 1024 ? 4 : 16;  // 32 would spill to AGPRs; 8 at 1024 to scratch
+    int L = 4;
+    while (L < LMAX && NT * L < p.k) L *= 2;
+    if (NT * L < p.k) return false;
+    const dim3 grid(p.n / kStrip);
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(NT), 0, s, p); };
+    auto pick = [&](auto tail) {
+        constexpr bool T = decltype(tail)::value;
+        switch (L) {
+            case 4: return go(gemv_row_kernel<NT, 4, NORM, T>);
+            case 8:
+                if constexpr (LMAX >= 8) return go(gemv_row_kernel<NT, 8, NORM, T>);
+                break;
+            default:
+                if constexpr (LMAX >= 16) return go(gemv_row_kernel<NT, 16, NORM, T>);
+                break;
+        }
+    };
+    if (NT * L == p.k) pick(std::false_type{});
+    else pick(std::true_type{});
+    return true;
+}
+
+// Threads per workgroup of gemv_row_kernel: EM_PACKED_THREADS (256, 512 or
+// 1024) when set, else 512 above 2048 rows of k and 256 up to it.
+int row_threads(int k) {
+    static const int env = [] {
+        const char* v = std::getenv("EM_PACKED_THREADS");
+        const int x = v ? std::atoi(v) : 0;
+        return x == 256 || x == 512 || x == 1024 ? x : 0;
+    }();
+    return env ? env : k > 2048 ? 512 : 256;
+}
+
+// EM_PACKED_ROW=0 sends one-row products back to gemv_packed_kernel (A
+// staged in LDS), for comparisons.
+bool row_kernel_enabled() {
+    static const bool on = [] {
+        const char* v = std::getenv("EM_PACKED_ROW");
+        return !(v && std::string(v) == "0");
+    }();
+    return on;
+}
+
 template <bool NORM, bool VEC>
 void launch_threads(const PackedParams& p, hipStream_t s) {
+    if (p.m == 1 && VEC && row_kernel_enabled()) {
+        // 512 threads (two waves per SIMD, one multiplying while the other
+        // waits for its loads) above 2048 rows of k, 256 up to it (4096^2:
+        // 4.7 against 4.9 us; 2048 x 8192: 4.8 against 4.7); at most 4096
+        // rows at 256 threads (1024 by request), 8192 at 512. Deeper k loops
+        // in gemv_packed_kernel.
+        const int nt = row_threads(p.k);
+        if (nt == 1024 && launch_row<1024, NORM>(p, s)) return;
+        if (nt == 256 && launch_row<256, NORM>(p, s)) return;
+        if (launch_row<512, NORM>(p, s)) return;
+    }
     if (p.m <= 1) {
         // Past 8192 rows a 256-thread workgroup would loop over batches;
         // 512 threads hold up to 16384 rows in one batch.
