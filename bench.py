@@ -55,11 +55,11 @@ EXACT_SPLIT_PEAK_TFLOPS = BF16_MFMA_PEAK_TFLOPS / 3
 def q8_kernel(m: int, k: int = 4096, n: int = 4096, registered: bool = False) -> tuple:
     """(kernel name, compute peak in TFLOP/s) that automatic uses for int8 B.
     Registered weights (em_q8_register, as DeviceQTensor does): one row runs
-    the strip-copy GEMV, 2 - 4 rows (k <= 4096) and 5 - 8 rows (k, n <= 4096)
+    the strip-copy GEMV (k <= 8192, or 12288 with n >= 4096: no norm here), 2 - 4 rows (k <= 4096) and 5 - 8 rows (k, n <= 4096)
     the strip-copy MFMA kernel (decode_mfma_supported). Otherwise (and
     unregistered): the GEMV up to 4 rows of small weights, the exact-split
     kernel from 5 rows (split_bf16_preferred)."""
-    if registered and m == 1 and k <= 8192:
+    if registered and m == 1 and (k <= 8192 or (k <= 12288 and n >= 4096)):
         return "strip-copy GEMV (fp32 VALU)", FP32_MFMA_PEAK_TFLOPS / 2
     if registered and 2 <= m <= 8 and k <= 4096 and k % 4 == 0 and (
             m <= 2 or (m <= 4 and n <= 24576) or n <= 4096):

@@ -123,7 +123,8 @@ int em_unpack_q8(size_t k, size_t n, const int8_t* packed, int8_t* B, void* stre
 /* Registers row-major int8 weights B (k x n, device memory) for em_matmul_q8:
  * the library keeps a strip-layout copy, packed from B's bytes on `stream`
  * (then drained), and em_matmul_q8 runs decode-shaped products over that
- * copy in one launch: one row (m == 1, k <= 8192) with EM_KERNEL_AUTOMATIC
+ * copy in one launch: one row (m == 1, k <= 8192, or k <= 12288 without a
+ * norm weight when n >= 4096) with EM_KERNEL_AUTOMATIC
  * or EM_KERNEL_SKINNY, and, with EM_KERNEL_AUTOMATIC, 2 - 8 rows at
  * k <= 4096 (3 - 4 rows up to n = 24576, 5 - 8 up to n = 4096; A 16-byte
  * aligned). Same

@@ -64,13 +64,19 @@ const int8_t* strip_copy_of(const void* B, std::size_t k, std::size_t n) {
 }
 
 // One-row products over registered weights run the strip-layout GEMV: one
-// launch and no split-K partials. Up to 8192 rows of B (one batch of a
-// 256-thread workgroup) it beat the row-major split-K call at every width
-// measured (4096^2: 4.8-4.9 against 6.5 us; 4096 x 11008: 10.0 against
-// 11.8; 4096 x 32000: 23.2 against 25.4); at 11008 rows it lost (13.7
-// against 11.6), and from two rows the GEMV's multiply-adds per byte grow
-// with m and the row-major kernels win.
-constexpr std::size_t kStripMaxK = 8192;
+// launch and no split-K partials. Up to 8192 rows of B it beat the
+// row-major split-K call at every width measured (4096^2: 4.6 against 6.5
+// us; 4096 x 11008: 9.1 against 11.8; 4096 x 32000: 21.8 against 25.4),
+// and without a norm up to 12288 rows when B has at least 4096 columns
+// (one pass of gemv_row_kernel at 512 threads, one workgroup per strip:
+// 11008 x 4096 10.6 against 11.9, 12288 x 4096 10.9 against 12.2; with 64
+// strips, 11008 x 1024, 7.5 against 7.0). Deeper, the strip kernel loops
+// over batches and lost (11008 rows before the one-pass kernel: 13.7
+// against 11.6); from two rows the GEMV's multiply-adds per byte grow with
+// m and the row-major kernels win.
+bool strip_row_takes(std::size_t k, std::size_t n, bool norm) {
+    return k <= 8192 || (!norm && k <= 12288 && n >= 4096);
+}
 
 // Decode batches (2 .. 16 rows) over registered weights: decode_mfma.hip.
 // EM_DECODE_MFMA=0 keeps them on the row-major kernels.
@@ -147,7 +153,7 @@ int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, co
         a.rms_weight = rms_weight;
         a.stream = s;
         if (std::is_same<BT, int8_t>::value && kernel == EM_KERNEL_SKINNY && m == 1 &&
-            k <= kStripMaxK) {
+            strip_row_takes(k, n, rms_weight != nullptr)) {
             if (const int8_t* P = strip_copy_of(B, k, n)) {
                 run_gemv_packed(a, P);
                 hip_check(hipGetLastError(), "launch");

@@ -3,8 +3,9 @@
 // (the reference keeps QTensor row-major, tensor.h:23-28, and its decode
 // product is sgemm_skinny + sum_slices, cuda_matmul.cu:189-254, 365-397).
 // This file holds the layout and the VALU products over it: one row of A
-// up to k = 8192 in gemv_row_kernel (A loaded beside each weight unit),
-// and in gemv_packed_kernel (A staged in LDS per batch) deeper k, A not
+// up to k = 12288 (8192 with a fused norm) in gemv_row_kernel (A loaded
+// beside each weight unit), and in gemv_packed_kernel (A staged in LDS per
+// batch) deeper k, A not
 // 16-byte aligned, and the 2 .. 8 row shapes that the MFMA kernel over the
 // same layout (decode_mfma.hip) does not take.
 //
@@ -476,13 +477,16 @@ int packed_depth(int nt, int k, int lmax) {
 // may also run 512 or 1024 threads per strip, with 8192 / NT rows per lane
 // at most (the same rows per batch, the register budget per lane shrinking
 // with the waves per SIMD).
-// gemv_row_kernel at NT threads: the shallowest L (4 .. LMAX) whose NT x L
-// units hold all of k; false when k is deeper than that.
+// gemv_row_kernel at NT threads: the shallowest L (4, 8, 16, then 24 at 512
+// threads without a norm) whose NT x L units hold all of k; false when k is
+// deeper than that.
 template <int NT, bool NORM>
 bool launch_row(const PackedParams& p, hipStream_t s) {
-    constexpr int LMAX = NT == 1024 ? 4 : 16;  // 32 would spill to AGPRs; 8 at 1024 to scratch
+    // Deeper lanes spill: 32 units to AGPRs, 24 with the norm weight's
+    // registers (or 8 at 1024 threads) to scratch.
+    constexpr int LMAX = NT == 1024 ? 4 : NT == 512 && !NORM ? 24 : 16;
     int L = 4;
-    while (L < LMAX && NT * L < p.k) L *= 2;
+    while (L < LMAX && NT * L < p.k) L = L < 16 ? 2 * L : L + 8;
     if (NT * L < p.k) return false;
     const dim3 grid(p.n / kStrip);
     auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(NT), 0, s, p); };
@@ -493,8 +497,11 @@ bool launch_row(const PackedParams& p, hipStream_t s) {
             case 8:
                 if constexpr (LMAX >= 8) return go(gemv_row_kernel<NT, 8, NORM, T>);
                 break;
-            default:
+            case 16:
                 if constexpr (LMAX >= 16) return go(gemv_row_kernel<NT, 16, NORM, T>);
+                break;
+            default:
+                if constexpr (LMAX >= 24) return go(gemv_row_kernel<NT, 24, NORM, T>);
                 break;
         }
     };
@@ -530,8 +537,8 @@ void launch_threads(const PackedParams& p, hipStream_t s) {
         // 512 threads (two waves per SIMD, one multiplying while the other
         // waits for its loads) above 2048 rows of k, 256 up to it (4096^2:
         // 4.7 against 4.9 us; 2048 x 8192: 4.8 against 4.7); at most 4096
-        // rows at 256 threads (1024 by request), 8192 at 512. Deeper k loops
-        // in gemv_packed_kernel.
+        // rows at 256 threads (1024 by request), 8192 at 512 (12288 without
+        // a norm). Deeper k loops in gemv_packed_kernel.
         const int nt = row_threads(p.k);
         if (nt == 1024 && launch_row<1024, NORM>(p, s)) return;
         if (nt == 256 && launch_row<256, NORM>(p, s)) return;

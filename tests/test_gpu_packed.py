@@ -77,10 +77,12 @@ def test_pack_rejects_k_not_a_multiple_of_4():
 
 # (m, k, n): decode rows 1..8 against the stories15M and Llama-7B-shaped
 # projections, a k that needs several 4096-row batches (11008, 8196), k
-# below one batch or not a multiple of 256, and k past the MFMA kernel's
-# 4096 at 2 .. 8 rows (4100, 11008: the VALU kernel).
+# below one batch or not a multiple of 256, the deepest one-row pass
+# without a norm (12288) and one quad past it, and k past the MFMA
+# kernel's 4096 at 2 .. 8 rows (4100, 11008: the VALU kernel).
 SHAPES = [(1, 288, 864), (1, 288, 32000), (1, 768, 288), (1, 4096, 4096), (1, 11008, 4096),
-          (1, 8196, 64), (1, 4, 16), (1, 20, 48), (2, 300, 1536), (3, 4096, 272),
+          (1, 8196, 64), (1, 12288, 48), (1, 12292, 32), (1, 4, 16), (1, 20, 48),
+          (2, 300, 1536), (3, 4096, 272),
           (4, 4100, 32), (5, 516, 2048), (8, 1000, 4096), (8, 11008, 64), (6, 20, 16),
           (7, 4, 160), (2, 4096, 4096), (4, 4096, 11008), (8, 4096, 4096), (5, 288, 32000)]
 
@@ -162,7 +164,8 @@ def test_packed_graph_replay_matches_eager():
 
 # ---- registered weights: em_matmul_q8 over the strip copy -------------------
 
-REG_SHAPES = [(288, 864), (4096, 4096), (8192, 64), (768, 288), (288, 32000), (20, 48)]
+REG_SHAPES = [(288, 864), (4096, 4096), (8192, 64), (11008, 64), (11008, 4096), (768, 288),
+              (288, 32000), (20, 48)]
 
 
 @pytest.mark.parametrize("kernel", ["automatic", "skinny"])
@@ -184,11 +187,14 @@ def test_registered_one_row_against_oracle(shape, fusion, kernel):
         wd = dev(w) if rms else None
         em.matmul(dev(A), qd, C, scale=sd, kernel=kernel, accumulate=acc, rms_weight=wd)
         got = host(C)
-        # The registered call is the strip-layout product, bit for bit.
-        P = em.pack_q8(qd)
-        C2 = dev(C0) if acc else torch.empty((1, n), device="cuda")
-        em.matmul_packed(dev(A), P, n, sd, C2, accumulate=acc, rms_weight=wd)
-        assert np.array_equal(got, host(C2))
+        # Where the registered call takes the strip copy (k <= 8192, or
+        # 12288 without a norm and with n >= 4096), it is the strip-layout
+        # product, bit for bit; otherwise it is the row-major call.
+        if k <= 8192 or (not rms and k <= 12288 and n >= 4096):
+            P = em.pack_q8(qd)
+            C2 = dev(C0) if acc else torch.empty((1, n), device="cuda")
+            em.matmul_packed(dev(A), P, n, sd, C2, accumulate=acc, rms_weight=wd)
+            assert np.array_equal(got, host(C2))
     finally:
         em.unregister_q8(qd)
     assert not em.registered_q8(qd)
