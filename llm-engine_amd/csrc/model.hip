@@ -16,7 +16,11 @@
 // At decode sizes (m <= 8) the qkv and w13 GEMVs leave their k-slice
 // partials to rope_cache_kernel and swiglu_kernel, which add them in slice
 // order and scale them exactly as reduce_slices would: the same bits, two
-// dependent launches fewer per layer.
+// dependent launches fewer per layer. An int8 model whose projections took
+// strip-layout copies at load (em_q8_register) runs its one-token steps as
+// one em_matmul_q8 call per product over them instead: each a single launch
+// with the norm or the residual add inside, so no partials and no slice
+// reduces.
 //
 // Kernels read the position and tokens from the device feed, so the first
 // one-token call is run eagerly and then captured into a HIP graph that
@@ -290,6 +294,13 @@ private:
     // prefill rows writes qkv_ and rope_cache_kernel follows, rather than
     // RoPE and the cache write in the product's epilogue (tests).
     bool rope_fusion_ = true;
+    // int8 models whose five projections all took a strip-layout copy
+    // (em_q8_register): one-token steps run every product as one
+    // em_matmul_q8 call over it (norm fused, no k slices), the attention
+    // merging its own chunks and swiglu_kernel between w13 and w2.
+    // EM_MODEL_STRIPS=0 at creation keeps the row-major decode path.
+    bool strips_ = false;
+    void register_strips();
     Buf<float> ssq_;
 
     Pinned<int> feed_host_;  // [pos, tokens...]
@@ -360,7 +371,32 @@ void Model::init_runtime() {
     const char* rf = std::getenv("EM_PREFILL_ROPE_FUSION");
     rope_fusion_ = !rf || std::atoi(rf) != 0;
     check(hipStreamSynchronize(stream_), "load weights");
+    register_strips();
     reserve_rows(1);
+}
+
+// Every int8 projection gets a strip-layout copy, or none does (a shape
+// the layout cannot hold, or EM_MODEL_STRIPS=0 / EM_STRIP_COPY=0).
+void Model::register_strips() {
+    const char* env = std::getenv("EM_MODEL_STRIPS");
+    if (!q8_ || (env && std::atoi(env) == 0)) return;
+    std::vector<const Proj*> all{&wcls_};
+    for (const LayerDev& L : layers_) {
+        all.push_back(&L.wqkv);
+        all.push_back(&L.wo);
+        all.push_back(&L.w13);
+        all.push_back(&L.w2);
+    }
+    bool every = true;
+    for (const Proj* p : all) {
+        if (em_q8_register(p->q8.p, p->rows, p->cols, stream_) != EM_OK) throw DeviceError(em_last_error());
+        every = every && em_q8_registered(p->q8.p, p->rows, p->cols) == 1;
+    }
+    if (!every) {
+        for (const Proj* p : all) em_q8_unregister(p->q8.p);
+        return;
+    }
+    strips_ = true;
 }
 
 // ---- llama2.c v0 checkpoint ---------------------------------------------
@@ -629,7 +665,18 @@ int Model::read_weight(const std::string& name, std::size_t layer, void* dst, st
     return EM_OK;
 }
 
-Model::~Model() { (void)hipStreamSynchronize(stream_); }
+Model::~Model() {
+    (void)hipStreamSynchronize(stream_);
+    if (strips_) {
+        (void)em_q8_unregister(wcls_.q8.p);
+        for (const LayerDev& L : layers_) {
+            (void)em_q8_unregister(L.wqkv.q8.p);
+            (void)em_q8_unregister(L.wo.q8.p);
+            (void)em_q8_unregister(L.w13.q8.p);
+            (void)em_q8_unregister(L.w2.q8.p);
+        }
+    }
+}
 
 void Model::upload(Buf<float>& b, const float* src, std::size_t count) {
     b.alloc(count);
@@ -792,14 +839,38 @@ void Model::enqueue(int n) {
     check(hipMemcpyAsync(feed_dev_.p, feed_host_.p, (n + 1) * sizeof(int), hipMemcpyHostToDevice,
                          stream_),
           "upload feed");
-    // One-token steps hand the norm GEMVs the sums of squares of x from
-    // whichever kernel last wrote x (embed, or a residual reduce).
-    bool have_ssq = n == 1 && use_ssq_;
+    // One-token steps over strip copies: each product is one em_matmul_q8
+    // call (the norm formed inside it). Other one-token steps hand the norm
+    // GEMVs the sums of squares of x from whichever kernel last wrote x
+    // (embed, or a residual reduce).
+    const bool strip_step = n == 1 && strips_;
+    bool have_ssq = n == 1 && use_ssq_ && !strip_step;
     hipLaunchKernelGGL(embed_kernel, dim3(ceil_div(ceil_div(D, 4), kThreads), n), dim3(kThreads), 0,
                        stream_, D, feed_dev_.p, emb_.p, x_.p, have_ssq ? ssq_.p : nullptr);
     const int rope_threads = D / 2 + KV / 2 + KV;
     const int swiglu_blocks = std::min(ceil_div(static_cast<long long>(n) * H, kThreads), 4096);
     for (LayerDev& L : layers_) {
+        if (strip_step) {
+            project(1, x_.p, L.wqkv, qkv_.p, L.rms_att.p, false);
+            const Summed qkv{qkv_.p, nullptr, nullptr, 1, qkv_cols,
+                             static_cast<std::size_t>(qkv_cols)};
+            if (!run_attention_rope(shape_, feed_dev_.p, qkv, D, KV, rope_cos_.p, rope_sin_.p,
+                                    L.kcache.p, L.vcache.p, att_.p, attn_scratch_.p, stream_)) {
+                hipLaunchKernelGGL(rope_cache_kernel, dim3(ceil_div(rope_threads, kThreads), 1),
+                                   dim3(kThreads), 0, stream_, qkv, qkv_cols, D, KV, hs,
+                                   feed_dev_.p, rope_cos_.p, rope_sin_.p, qkv_.p, L.kcache.p,
+                                   L.vcache.p);
+                run_attention(shape_, 1, feed_dev_.p, qkv_.p, L.kcache.p, L.vcache.p, att_.p,
+                              attn_scratch_.p, kAttnAutomatic, stream_);
+            }
+            project(1, att_.p, L.wo, x_.p, nullptr, true);
+            project(1, x_.p, L.w13, gu_.p, L.rms_ffn.p, false);
+            const Summed gu{gu_.p, nullptr, nullptr, 1, 2 * H, static_cast<std::size_t>(2 * H)};
+            hipLaunchKernelGGL(swiglu_kernel, dim3(swiglu_blocks), dim3(kThreads), 0, stream_, 1,
+                               H, gu, hb_.p);
+            project(1, hb_.p, L.w2, x_.p, nullptr, true);
+            continue;
+        }
         bool roped = false;
         Summed qkv{qkv_.p, nullptr, nullptr, 1, qkv_cols,
                    static_cast<std::size_t>(n) * qkv_cols};

@@ -181,6 +181,53 @@ def test_decode_merge_inside_wo_gemv(tmp_path, monkeypatch, dim, hidden, heads, 
     merged_first.close()
 
 
+@pytest.mark.parametrize("dim,hidden,heads,kv_heads",
+                         [(256, 688, 4, 2), (320, 864, 5, 5), (192, 512, 6, 2)],
+                         ids=["d256_gqa", "d320_mha", "d192_group3"])
+def test_strip_copy_decode_matches_cpu(tmp_path, monkeypatch, dim, hidden, heads, kv_heads):
+    # int8 with a vocabulary of 320 (a multiple of 16): every projection
+    # takes a strip-layout copy, so one-token steps run each product as one
+    # em_matmul_q8 call over it (norm and residual inside, the attention
+    # merging its own chunks). A second model created with
+    # EM_MODEL_STRIPS=0 runs the row-major decode path. Every decode over
+    # the context, then a chunked and a whole prefill (row-major either way),
+    # each model against the CPU Transformer within the 3e-5 of the largest
+    # logit used above, greedy token equal.
+    m = e2e_model.fixture_model(heads, kv_heads, False, seed=dim + 3 * heads, dim=dim,
+                                hidden=hidden, vocab=320, seq_len=24)
+    path = str(tmp_path / "model.bin")
+    e2e_model.write_raw(path, m)
+    ck = oracle.RefCheckpoint(lib, path)
+    w = ck.weights()
+    cpu = oracle.RefTransformer(lib, ck, True)
+    strips = em.Model(ck.config, w, q8=True)
+    monkeypatch.setenv("EM_MODEL_STRIPS", "0")
+    rowmajor = em.Model(ck.config, w, q8=True)
+    monkeypatch.delenv("EM_MODEL_STRIPS")
+    T, V = ck.config["seq_len"], ck.config["vocab_size"]
+    tokens = [(p * 7 + 3) % V for p in range(T)]
+
+    def near(g, c, what):
+        tol = 3e-5 * float(np.abs(c).max())
+        d = float(np.abs(g - c).max())
+        assert d <= tol, f"{what}: max diff {d} > {tol}"
+        assert int(np.argmax(g)) == int(np.argmax(c)), f"{what}: greedy token"
+
+    for pos in range(T):
+        print(f"strip decode dim {dim} pos {pos}", flush=True)
+        c = cpu.run([tokens[pos]], pos, True)
+        near(strips.forward(tokens[pos], pos), c, f"strips at {pos}")
+        near(rowmajor.forward(tokens[pos], pos), c, f"row-major at {pos}")
+    c = cpu.run(tokens[:7], 0)
+    near(strips.forward(tokens[:7], 0), c, "prefill 7")
+    c = cpu.run([tokens[7]], 7, True)
+    near(strips.forward(tokens[7], 7), c, "decode after prefill")
+    c = cpu.run(tokens, 0)
+    near(strips.forward(tokens, 0), c, "full prefill")
+    strips.close()
+    rowmajor.close()
+
+
 @pytest.mark.parametrize("heads,kv_heads", [(4, 4), (4, 2)], ids=["mha", "gqa"])
 def test_prefill_rope_epilogue_same_bits_as_rope_kernel(tmp_path, monkeypatch, heads, kv_heads):
     # Int8 prefill rows send the fused qkv product to the exact-split kernel;
