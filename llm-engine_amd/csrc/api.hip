@@ -90,6 +90,10 @@ bool decode_mfma_enabled() {
 
 }  // namespace
 
+const int8_t* registered_strip(const void* B, std::size_t k, std::size_t n) {
+    return strip_copy_of(B, k, n);
+}
+
 // The matmul entry points. `workspace` (em_matmul_q8_noalloc, with the
 // skinny kernel): called once the shape is valid and a GPU is present, it
 // returns the caller's buffer for split-K partials and its size in floats;

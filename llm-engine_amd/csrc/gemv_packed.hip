@@ -342,38 +342,53 @@ __global__ __launch_bounds__(NT) void gemv_packed_kernel(PackedParams p) {
 // beside A and multiplied in; the row's sum of squares is formed on the
 // way (counted from the c == 0 lanes, which between them hold each A value
 // once) and its RMS scale multiplies each reduced sum once.
-template <int NT, int L, bool NORM, bool TAIL>
+// PAIR (one row of A over a matrix of 2h columns, h % 16 == 0, whose
+// first h columns are gates and last h ups, as the forward pass's w13):
+// workgroup j takes strips j and j + h / 16 with the same A values and
+// writes silu(gate) * up for columns 16j .. 16j + 15 of an h-wide output,
+// not the product. Each half is summed in the order the unpaired kernel
+// sums it, so the result has the bits of the product followed by the
+// SwiGLU, one launch fewer.
+template <int NT, int L, bool NORM, bool TAIL, bool PAIR = false>
 __global__ __launch_bounds__(NT) void gemv_row_kernel(PackedParams p) {
     constexpr int NW = NT / kWave;
-    __shared__ float red[NW][kStrip + 1];
+    constexpr int NH = PAIR ? 2 : 1;  // strips per workgroup
+    __shared__ float red[NW][NH * kStrip + 1];
     const int tid = threadIdx.x;
     const int c = tid & 3;
     const int strip = blockIdx.x;
+    const int pair_off = PAIR ? p.n / (2 * kStrip) : 0;  // the up strip, strips after the gate
     const int8_t* base = p.P + static_cast<size_t>(strip) * p.k * kStrip;
     float4 av[L];
     float4 nv[NORM ? L : 1];
-    uint4 w[L];
+    uint4 w[NH][L];
 #pragma unroll
     for (int i = 0; i < L; ++i) {
         const int u = tid + i * NT;
         const int uc = TAIL ? min(u, p.k - 4 + c) : u;
         av[i] = *reinterpret_cast<const float4*>(p.A + (uc & ~3));
         if constexpr (NORM) nv[i] = *reinterpret_cast<const float4*>(p.rms_weight + (uc & ~3));
-        w[i] = stream_load(reinterpret_cast<const uint4*>(base + static_cast<size_t>(uc) * kStrip));
+        w[0][i] = stream_load(reinterpret_cast<const uint4*>(base + static_cast<size_t>(uc) * kStrip));
+        if constexpr (PAIR)
+            w[NH - 1][i] = stream_load(reinterpret_cast<const uint4*>(
+                base + (static_cast<size_t>(pair_off) * p.k + uc) * kStrip));
     }
     // The epilogue's scale (and prior C) behind the weights, waited for at
     // the end.
     __builtin_amdgcn_sched_barrier(0);
     const int ec = strip * kStrip + tid % kStrip;
     const float esc = p.scale[ec];
-    const float eprior = p.accumulate ? p.C[ec] : 0.0f;
+    const float esc_up = PAIR ? p.scale[ec + pair_off * kStrip] : 0.0f;
+    const float eprior = !PAIR && p.accumulate ? p.C[ec] : 0.0f;
     __builtin_amdgcn_sched_barrier(0);
 
-    float acc[4][4];
+    float acc[NH][4][4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int h = 0; h < NH; ++h)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[t][u] = 0.0f;
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[h][t][u] = 0.0f;
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < L; ++i) {
@@ -391,42 +406,62 @@ __global__ __launch_bounds__(NT) void gemv_row_kernel(PackedParams p) {
                 a[t] *= g[t];
             }
         }
-        float bv[4][4];  // [row t of the quad][column 4c + u]
-        widen4(w[i].x, bv[0]);
-        widen4(w[i].y, bv[1]);
-        widen4(w[i].z, bv[2]);
-        widen4(w[i].w, bv[3]);
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int h = 0; h < NH; ++h) {
+            float bv[4][4];  // [row t of the quad][column 4c + u]
+            widen4(w[h][i].x, bv[0]);
+            widen4(w[h][i].y, bv[1]);
+            widen4(w[h][i].z, bv[2]);
+            widen4(w[h][i].w, bv[3]);
 #pragma unroll
-            for (int u = 0; u < 4; ++u) acc[t][u] = fmaf(a[t], bv[t][u], acc[t][u]);
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) acc[h][t][u] = fmaf(a[t], bv[t][u], acc[h][t][u]);
+        }
     }
 
     // Column 4c + u summed over the quad's rows, then over the wave's 16
     // lanes with the same c (lane_reduce16), then over the waves in order.
     const int wave = tid / kWave, lane = tid % kWave;
-    float v[4], o[1];
+    float v[4 * NH], o[1];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = ((acc[0][u] + acc[1][u]) + acc[2][u]) + acc[3][u];
-    lane_reduce16<4>(v, o);
-    if (lane_writes<4>(lane)) red[wave][4 * c + lane_item<4>(lane, 0)] = o[0];
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            v[4 * h + u] = ((acc[h][0][u] + acc[h][1][u]) + acc[h][2][u]) + acc[h][3][u];
+    lane_reduce16<4 * NH>(v, o);
+    if (lane_writes<4 * NH>(lane)) {
+        const int item = lane_item<4 * NH>(lane, 0);  // half item / 4, column 4c + item % 4
+        red[wave][(item / 4) * kStrip + 4 * c + item % 4] = o[0];
+    }
     if constexpr (NORM) {
         const float sw = wave_sum(c == 0 ? ss : 0.0f);
-        if (lane == 0) red[wave][kStrip] = sw;
+        if (lane == 0) red[wave][NH * kStrip] = sw;
     }
     __syncthreads();
     if (tid < kStrip) {
-        float total = red[0][tid];
+        float total[NH];
 #pragma unroll
-        for (int w2 = 1; w2 < NW; ++w2) total += red[w2][tid];
-        if constexpr (NORM) {
-            float sq = red[0][kStrip];
+        for (int h = 0; h < NH; ++h) {
+            total[h] = red[0][h * kStrip + tid];
 #pragma unroll
-            for (int w2 = 1; w2 < NW; ++w2) sq += red[w2][kStrip];
-            total *= 1.0f / sqrtf(sq / static_cast<float>(p.k) + kRmsEps);
+            for (int w2 = 1; w2 < NW; ++w2) total[h] += red[w2][h * kStrip + tid];
         }
-        total *= esc;
-        p.C[ec] = p.accumulate ? eprior + total : total;
+        if constexpr (NORM) {
+            float sq = red[0][NH * kStrip];
+#pragma unroll
+            for (int w2 = 1; w2 < NW; ++w2) sq += red[w2][NH * kStrip];
+            const float rs = 1.0f / sqrtf(sq / static_cast<float>(p.k) + kRmsEps);
+#pragma unroll
+            for (int h = 0; h < NH; ++h) total[h] *= rs;
+        }
+        total[0] *= esc;
+        if constexpr (PAIR) {
+            total[NH - 1] *= esc_up;
+            p.C[ec] = silu_mul(total[0], total[NH - 1]);
+        } else {
+            p.C[ec] = p.accumulate ? eprior + total[0] : total[0];
+        }
     }
 }
 
@@ -478,30 +513,31 @@ int packed_depth(int nt, int k, int lmax) {
 // at most (the same rows per batch, the register budget per lane shrinking
 // with the waves per SIMD).
 // gemv_row_kernel at NT threads: the shallowest L (4, 8, 16, then 24 at 512
-// threads without a norm) whose NT x L units hold all of k; false when k is
-// deeper than that.
-template <int NT, bool NORM>
+// threads without a norm; at most 8 for PAIR) whose NT x L units hold all
+// of k; false when k is deeper than that.
+template <int NT, bool NORM, bool PAIR = false>
 bool launch_row(const PackedParams& p, hipStream_t s) {
     // Deeper lanes spill: 32 units to AGPRs, 24 with the norm weight's
-    // registers (or 8 at 1024 threads) to scratch.
-    constexpr int LMAX = NT == 1024 ? 4 : NT == 512 && !NORM ? 24 : 16;
+    // registers (or 8 at 1024 threads, or 16 of each half of a pair) to
+    // scratch.
+    constexpr int LMAX = NT == 1024 ? 4 : PAIR ? 8 : NT == 512 && !NORM ? 24 : 16;
     int L = 4;
     while (L < LMAX && NT * L < p.k) L = L < 16 ? 2 * L : L + 8;
     if (NT * L < p.k) return false;
-    const dim3 grid(p.n / kStrip);
+    const dim3 grid(p.n / (PAIR ? 2 * kStrip : kStrip));
     auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(NT), 0, s, p); };
     auto pick = [&](auto tail) {
         constexpr bool T = decltype(tail)::value;
         switch (L) {
-            case 4: return go(gemv_row_kernel<NT, 4, NORM, T>);
+            case 4: return go(gemv_row_kernel<NT, 4, NORM, T, PAIR>);
             case 8:
-                if constexpr (LMAX >= 8) return go(gemv_row_kernel<NT, 8, NORM, T>);
+                if constexpr (LMAX >= 8) return go(gemv_row_kernel<NT, 8, NORM, T, PAIR>);
                 break;
             case 16:
-                if constexpr (LMAX >= 16) return go(gemv_row_kernel<NT, 16, NORM, T>);
+                if constexpr (LMAX >= 16) return go(gemv_row_kernel<NT, 16, NORM, T, PAIR>);
                 break;
             default:
-                if constexpr (LMAX >= 24) return go(gemv_row_kernel<NT, 24, NORM, T>);
+                if constexpr (LMAX >= 24) return go(gemv_row_kernel<NT, 24, NORM, T, PAIR>);
                 break;
         }
     };
@@ -571,6 +607,39 @@ void run_pack_strips(int k, int n, const int8_t* B, int8_t* P, hipStream_t strea
                                                             static_cast<long long>(cu_count()) * 16));
     hipLaunchKernelGGL(pack_strips_kernel, dim3(blocks > 0 ? blocks : 1), dim3(kThreads), 0, stream,
                        k, n, B, P);
+}
+
+bool gemv_swiglu_supported(const MatmulArgs& a) {
+    const int half = a.n / 2;
+    const int nt = row_threads(a.k);
+    const int deepest = nt == 1024 ? 1024 * 4 : nt * 8;
+    return a.m == 1 && a.n % (2 * kStrip) == 0 && a.k % 4 == 0 && half > 0 && a.k <= deepest &&
+           reinterpret_cast<uintptr_t>(a.A) % 16 == 0 && !a.accumulate;
+}
+
+void run_gemv_swiglu(const MatmulArgs& a, const int8_t* packed) {
+    PackedParams p{};
+    p.m = 1;
+    p.n = a.n;
+    p.k = a.k;
+    p.A = a.A;
+    p.rms_weight = a.rms_weight;
+    p.P = packed;
+    p.scale = a.scale;
+    p.C = a.C;
+    p.accumulate = 0;
+    bool done = false;
+    const int nt = row_threads(a.k);
+    if (a.rms_weight) {
+        done = nt == 1024 ? launch_row<1024, true, true>(p, a.stream)
+               : nt == 256 ? launch_row<256, true, true>(p, a.stream)
+                           : launch_row<512, true, true>(p, a.stream);
+    } else {
+        done = nt == 1024 ? launch_row<1024, false, true>(p, a.stream)
+               : nt == 256 ? launch_row<256, false, true>(p, a.stream)
+                           : launch_row<512, false, true>(p, a.stream);
+    }
+    if (!done) throw DeviceError("gemv_swiglu: k too deep for one pass");
 }
 
 void run_unpack_strips(int k, int n, const int8_t* P, int8_t* B, hipStream_t stream) {

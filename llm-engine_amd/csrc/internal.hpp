@@ -195,6 +195,15 @@ void run_pack_strips(int k, int n, const int8_t* B, int8_t* P, hipStream_t strea
 void run_unpack_strips(int k, int n, const int8_t* P, int8_t* B, hipStream_t stream);
 // C (+)= rmsnorm?(A) x B for m <= 8 rows, B in the strip layout, one launch.
 void run_gemv_packed(const MatmulArgs& a, const int8_t* packed);
+// One row, B of 2h columns (gates, then ups) in the strip layout:
+// C[j] = silu(P[j]) * P[h + j] for j < h, P = rmsnorm?(A) x B, one launch,
+// the bits of run_gemv_packed followed by the SwiGLU. Supported: n a
+// multiple of 32, k % 4 == 0, k within one pass (4096 rows at 512 threads),
+// A 16-byte aligned, no accumulate.
+bool gemv_swiglu_supported(const MatmulArgs& a);
+void run_gemv_swiglu(const MatmulArgs& a, const int8_t* packed);
+// The strip-layout copy of registered int8 weights B (k x n), or null.
+const int8_t* registered_strip(const void* B, std::size_t k, std::size_t n);
 // 2 .. 8 rows over a strip-layout copy, fp32 MFMA, one launch
 // (decode_mfma.hip): n % 16 == 0, k % 4 == 0, k <= 4096, A 16-byte aligned.
 bool decode_mfma_supported(const MatmulArgs& a);

@@ -20,7 +20,7 @@
 // strip-layout copies at load (em_q8_register) runs its one-token steps as
 // one em_matmul_q8 call per product over them instead: each a single launch
 // with the norm or the residual add inside, so no partials and no slice
-// reduces.
+// reduces; w13's launch also forms the SwiGLU (run_gemv_swiglu).
 //
 // Kernels read the position and tokens from the device feed, so the first
 // one-token call is run eagerly and then captured into a HIP graph that
@@ -300,6 +300,10 @@ private:
     // merging its own chunks and swiglu_kernel between w13 and w2.
     // EM_MODEL_STRIPS=0 at creation keeps the row-major decode path.
     bool strips_ = false;
+    // Over the strips, w13 and the SwiGLU are one launch (run_gemv_swiglu:
+    // the same bits); EM_MODEL_SWIGLU_FUSION=0 at creation runs
+    // swiglu_kernel after the w13 product instead (tests).
+    bool swiglu_fusion_ = true;
     void register_strips();
     Buf<float> ssq_;
 
@@ -370,6 +374,8 @@ void Model::init_runtime() {
     merge_kernel_ = mk && std::atoi(mk) != 0;
     const char* rf = std::getenv("EM_PREFILL_ROPE_FUSION");
     rope_fusion_ = !rf || std::atoi(rf) != 0;
+    const char* sf = std::getenv("EM_MODEL_SWIGLU_FUSION");
+    swiglu_fusion_ = !sf || std::atoi(sf) != 0;
     check(hipStreamSynchronize(stream_), "load weights");
     register_strips();
     reserve_rows(1);
@@ -864,10 +870,18 @@ void Model::enqueue(int n) {
                               attn_scratch_.p, kAttnAutomatic, stream_);
             }
             project(1, att_.p, L.wo, x_.p, nullptr, true);
-            project(1, x_.p, L.w13, gu_.p, L.rms_ffn.p, false);
-            const Summed gu{gu_.p, nullptr, nullptr, 1, 2 * H, static_cast<std::size_t>(2 * H)};
-            hipLaunchKernelGGL(swiglu_kernel, dim3(swiglu_blocks), dim3(kThreads), 0, stream_, 1,
-                               H, gu, hb_.p);
+            const MatmulArgs a13 = gemv_args(1, x_.p, L.w13, hb_.p, L.rms_ffn.p, false, nullptr);
+            const int8_t* p13 = registered_strip(L.w13.q8.p, L.w13.rows, L.w13.cols);
+            if (swiglu_fusion_ && p13 && gemv_swiglu_supported(a13)) {
+                run_gemv_swiglu(a13, p13);
+                check(hipGetLastError(), "launch");
+            } else {
+                project(1, x_.p, L.w13, gu_.p, L.rms_ffn.p, false);
+                const Summed gu{gu_.p, nullptr, nullptr, 1, 2 * H,
+                                static_cast<std::size_t>(2 * H)};
+                hipLaunchKernelGGL(swiglu_kernel, dim3(swiglu_blocks), dim3(kThreads), 0, stream_,
+                                   1, H, gu, hb_.p);
+            }
             project(1, hb_.p, L.w2, x_.p, nullptr, true);
             continue;
         }

@@ -188,11 +188,13 @@ def test_strip_copy_decode_matches_cpu(tmp_path, monkeypatch, dim, hidden, heads
     # int8 with a vocabulary of 320 (a multiple of 16): every projection
     # takes a strip-layout copy, so one-token steps run each product as one
     # em_matmul_q8 call over it (norm and residual inside, the attention
-    # merging its own chunks). A second model created with
-    # EM_MODEL_STRIPS=0 runs the row-major decode path. Every decode over
-    # the context, then a chunked and a whole prefill (row-major either way),
-    # each model against the CPU Transformer within the 3e-5 of the largest
-    # logit used above, greedy token equal.
+    # merging its own chunks, w13 and the SwiGLU one launch). A second model
+    # created with EM_MODEL_STRIPS=0 runs the row-major decode path, a third
+    # with EM_MODEL_SWIGLU_FUSION=0 the strips with swiglu_kernel after the
+    # w13 product, which must give the fused model's logits bit for bit.
+    # Every decode over the context, then a chunked and a whole prefill
+    # (row-major either way), each model against the CPU Transformer within
+    # the 3e-5 of the largest logit used above, greedy token equal.
     m = e2e_model.fixture_model(heads, kv_heads, False, seed=dim + 3 * heads, dim=dim,
                                 hidden=hidden, vocab=320, seq_len=24)
     path = str(tmp_path / "model.bin")
@@ -204,6 +206,9 @@ def test_strip_copy_decode_matches_cpu(tmp_path, monkeypatch, dim, hidden, heads
     monkeypatch.setenv("EM_MODEL_STRIPS", "0")
     rowmajor = em.Model(ck.config, w, q8=True)
     monkeypatch.delenv("EM_MODEL_STRIPS")
+    monkeypatch.setenv("EM_MODEL_SWIGLU_FUSION", "0")
+    unfused = em.Model(ck.config, w, q8=True)
+    monkeypatch.delenv("EM_MODEL_SWIGLU_FUSION")
     T, V = ck.config["seq_len"], ck.config["vocab_size"]
     tokens = [(p * 7 + 3) % V for p in range(T)]
 
@@ -216,8 +221,11 @@ def test_strip_copy_decode_matches_cpu(tmp_path, monkeypatch, dim, hidden, heads
     for pos in range(T):
         print(f"strip decode dim {dim} pos {pos}", flush=True)
         c = cpu.run([tokens[pos]], pos, True)
-        near(strips.forward(tokens[pos], pos), c, f"strips at {pos}")
+        g = strips.forward(tokens[pos], pos)
+        near(g, c, f"strips at {pos}")
         near(rowmajor.forward(tokens[pos], pos), c, f"row-major at {pos}")
+        u = unfused.forward(tokens[pos], pos)
+        assert np.array_equal(g, u), f"SwiGLU fused against not at {pos}: {np.abs(g - u).max()}"
     c = cpu.run(tokens[:7], 0)
     near(strips.forward(tokens[:7], 0), c, "prefill 7")
     c = cpu.run([tokens[7]], 7, True)
@@ -226,6 +234,7 @@ def test_strip_copy_decode_matches_cpu(tmp_path, monkeypatch, dim, hidden, heads
     near(strips.forward(tokens, 0), c, "full prefill")
     strips.close()
     rowmajor.close()
+    unfused.close()
 
 
 @pytest.mark.parametrize("heads,kv_heads", [(4, 4), (4, 2)], ids=["mha", "gqa"])
