@@ -377,8 +377,8 @@ void Model::init_runtime() {
     const char* sf = std::getenv("EM_MODEL_SWIGLU_FUSION");
     swiglu_fusion_ = !sf || std::atoi(sf) != 0;
     check(hipStreamSynchronize(stream_), "load weights");
-    register_strips();
     reserve_rows(1);
+    register_strips();  // last: nothing after it can throw and skip the destructor
 }
 
 // Every int8 projection gets a strip-layout copy, or none does (a shape
@@ -393,13 +393,20 @@ void Model::register_strips() {
         all.push_back(&L.w13);
         all.push_back(&L.w2);
     }
+    // A copy left registered after its weights are freed could be found
+    // again by a later allocation at the same address: on any failure every
+    // registration made here is undone before the error propagates.
     bool every = true;
     for (const Proj* p : all) {
-        if (em_q8_register(p->q8.p, p->rows, p->cols, stream_) != EM_OK) throw DeviceError(em_last_error());
+        if (em_q8_register(p->q8.p, p->rows, p->cols, stream_) != EM_OK) {
+            const std::string msg = em_last_error();
+            for (const Proj* q : all) (void)em_q8_unregister(q->q8.p);
+            throw DeviceError(msg);
+        }
         every = every && em_q8_registered(p->q8.p, p->rows, p->cols) == 1;
     }
     if (!every) {
-        for (const Proj* p : all) em_q8_unregister(p->q8.p);
+        for (const Proj* p : all) (void)em_q8_unregister(p->q8.p);
         return;
     }
     strips_ = true;
