@@ -168,6 +168,39 @@ REG_SHAPES = [(288, 864), (4096, 4096), (8192, 64), (11008, 64), (11008, 4096), 
               (288, 32000), (20, 48)]
 
 
+@pytest.mark.parametrize("fusion", ["plain", "rms"])
+@pytest.mark.parametrize("shape", [(4096, 4096), (288, 864), (11008, 4096)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_registered_one_row_misaligned_a(shape, fusion):
+    # A one float past a 16-byte boundary: the one-pass kernel needs 16-byte
+    # A, so the call takes the kernel that stages A in LDS (or, past its
+    # depth, the row-major path); either way within the oracle's bound, and
+    # the same bits on a second call.
+    k, n = shape
+    A = inputs.uniform((1, k), -1.0, 1.0, 61)
+    q, s = orc.quantize_q8(inputs.normal((k, n), 0.02, 62))
+    rms = fusion == "rms"
+    w = inputs.uniform((k,), 0.5, 1.5, 63) if rms else None
+    qd, sd = dev(q), dev(s)
+    buf = torch.zeros((k + 1,), device="cuda")
+    buf[1:] = dev(A)[0]
+    Am = buf[1:].view(1, k)
+    assert Am.data_ptr() % 16 == 4
+    em.register_q8(qd)
+    try:
+        wd = dev(w) if rms else None
+        C = torch.empty((1, n), device="cuda")
+        em.matmul(Am, qd, C, scale=sd, rms_weight=wd)
+        got = host(C)
+        em.matmul(Am, qd, C, scale=sd, rms_weight=wd)
+        assert np.array_equal(got, host(C))
+    finally:
+        em.unregister_q8(qd)
+    want = orc.matmul_fused(A, Bq=q, scale=s, w=w)
+    An = orc.rmsnorm(A, w) if rms else A
+    check(got, want, An, orc.dequantize(q, s), k, 2.0 if rms else 1.0)
+
+
 @pytest.mark.parametrize("kernel", ["automatic", "skinny"])
 @pytest.mark.parametrize("fusion", ["plain", "acc", "rms", "rms_acc"])
 @pytest.mark.parametrize("shape", REG_SHAPES, ids=lambda s: "x".join(map(str, s)))
