@@ -43,21 +43,9 @@
 namespace em {
 namespace {
 
-constexpr int kMinChunk = kSplitMinChunk;  // positions per split workgroup, at least
 constexpr int kMaxSplits = 256;         // chunks per (row, head group), at most
 constexpr std::size_t kSplitMaxRows = 12;  // automatic: split up to this many rows, at most
 constexpr std::size_t kMaxLds = 64 * 1024;  // dynamic LDS per workgroup
-
-int split_count(int seq_len) {
-    const int s = (seq_len + kMinChunk - 1) / kMinChunk;
-    return s < kMaxSplits ? s : kMaxSplits;
-}
-
-__host__ __device__ __forceinline__ int chunk_size(int n_ctx, int splits) {
-    return split_chunk(n_ctx, splits);
-}
-
-int split_chunk_cap(const AttnShape& s) { return chunk_size(s.seq_len, split_count(s.seq_len)); }
 
 // Query heads per split workgroup: the most of 8, 4, 2, 1 that divides the
 // heads sharing a kv head.
@@ -66,6 +54,21 @@ int heads_per_block(const AttnShape& s) {
     for (int g : {8, 4, 2})
         if (group % g == 0) return g;
     return 1;
+}
+
+// Positions per split workgroup, at least (split_chunk).
+int min_chunk(const AttnShape& s) {
+    return heads_per_block(s) > 1 ? kSplitMinChunkGrouped : kSplitMinChunk;
+}
+
+int split_count(const AttnShape& s) {
+    const int mc = min_chunk(s);
+    const int n = (s.seq_len + mc - 1) / mc;
+    return n < kMaxSplits ? n : kMaxSplits;
+}
+
+int split_chunk_cap(const AttnShape& s) {
+    return split_chunk(s.seq_len, split_count(s), min_chunk(s));
 }
 
 std::size_t single_lds(const AttnShape& s) {
@@ -94,7 +97,7 @@ struct SplitScratch {
 };
 
 SplitScratch split_scratch(const AttnShape& s, std::size_t rows) {
-    const std::size_t blocks = rows * s.n_heads * split_count(s.seq_len);
+    const std::size_t blocks = rows * s.n_heads * split_count(s);
     auto up4 = [](std::size_t x) { return (x + 3) / 4 * 4; };
     SplitScratch l{};
     l.o = 0;
@@ -175,6 +178,7 @@ int resolve(int kernel, std::size_t rows, const AttnShape& s) {
 
 struct AttnArgs {
     int n_heads, head_size, group, seq_len, splits, chunk_cap, rows;
+    int min_chunk;   // split_chunk's least chunk for this shape
     int merge_from;  // the merge kernel takes rows of at least this many chunks (>= 2)
     int tile_chunk;  // tile kernel split over the context: positions per chunk (0: no split)
     int q_stride, kv_stride, out_stride;
@@ -223,15 +227,15 @@ constexpr int kRoundPerSlot = 8;
 template <int G, int LPP, int F, bool ROPE = false>
 __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
     constexpr int NS = kThreads / LPP;
-    constexpr int PP = kMinChunk / NS < kRoundPerSlot ? (kMinChunk / NS > 0 ? kMinChunk / NS : 1)
-                                                       : kRoundPerSlot;
+    constexpr int MC = G > 1 ? kSplitMinChunkGrouped : kSplitMinChunk;  // min_chunk of the shape
+    constexpr int PP = MC / NS < kRoundPerSlot ? (MC / NS > 0 ? MC / NS : 1) : kRoundPerSlot;
     constexpr int ROUND = NS * PP;
     extern __shared__ float lds[];
 
     const int hs = a.head_size, hs4 = hs / 4;
     const int hg = blockIdx.x, i = blockIdx.y, s = blockIdx.z;
     const int n_ctx = *a.pos + i + 1;
-    const int chunk = chunk_size(n_ctx, a.splits);
+    const int chunk = split_chunk(n_ctx, a.splits, a.min_chunk);
     const int t0 = s * chunk;
     if (t0 >= n_ctx) return;  // uniform across the workgroup
     const int len = min(chunk, n_ctx - t0);
@@ -466,7 +470,7 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
     const int h = blockIdx.x / groups, d0 = (blockIdx.x % groups) * dpw;
     const int i = blockIdx.y;
     const int n_ctx = *a.pos + i + 1;
-    const int chunk = a.tile_chunk ? a.tile_chunk : chunk_size(n_ctx, a.splits);
+    const int chunk = a.tile_chunk ? a.tile_chunk : split_chunk(n_ctx, a.splits, a.min_chunk);
     const int n = (n_ctx + chunk - 1) / chunk;
     if (n < a.merge_from) return;  // one chunk: written by the split kernel; few: by their consumer
     const std::size_t b = (static_cast<std::size_t>(i) * a.n_heads + h) * a.splits;
@@ -918,12 +922,13 @@ AttnArgs base_args(const AttnShape& s, int rows, const int* pos, const float* q,
     a.out = out;
     a.rows = rows;
     a.merge_from = 2;
+    a.min_chunk = min_chunk(s);
     return a;
 }
 
 void set_split(const AttnShape& s, int rows, float* scratch, AttnArgs& a) {
     const SplitScratch l = split_scratch(s, rows);
-    a.splits = split_count(s.seq_len);
+    a.splits = split_count(s);
     a.chunk_cap = split_chunk_cap(s);
     a.part_o = scratch + l.o;
     a.part_ml = reinterpret_cast<float2*>(scratch + l.ml);
@@ -999,7 +1004,7 @@ bool run_attention_rope(const AttnShape& s, const int* pos, const Summed& src, i
     }
     if (defer) {
         *defer = SplitRow{};
-        if (hold) *defer = SplitRow{a.part_o, a.part_ml, out, pos, a.splits, s.n_heads, s.head_size};
+        if (hold) *defer = SplitRow{a.part_o, a.part_ml, out, pos, a.splits, s.n_heads, s.head_size, a.min_chunk};
     }
     return true;
 }

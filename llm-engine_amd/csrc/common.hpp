@@ -270,10 +270,18 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f +
 // kSplitMinChunk positions per chunk, and a row of n_ctx positions over at
 // most `splits` chunks has ceil(n_ctx / split_chunk(n_ctx, splits)) of them
 // (cuda_attention.cu:25-31).
+//
+// The least chunk is 64 positions when each split workgroup serves one
+// query head, 32 when it serves a group of heads sharing a kv head (their
+// keys and values are a quarter or less of the bytes per position, so a
+// longer chunk mostly adds latency: 8 kv heads at contexts 128 / 512 / 1024
+// took 10.6 / 11.9 / 12.7 us with 64, 8.9 / 10.1 / 11.1 with 32; one head
+// per workgroup measured even or slower with 32 outside 256-512).
 constexpr int kSplitMinChunk = 64;
-__host__ __device__ __forceinline__ int split_chunk(int n_ctx, int splits) {
+constexpr int kSplitMinChunkGrouped = 32;
+__host__ __device__ __forceinline__ int split_chunk(int n_ctx, int splits, int min_chunk) {
     const int c = (n_ctx + splits - 1) / splits;
-    return c > kSplitMinChunk ? c : kSplitMinChunk;
+    return c > min_chunk ? c : min_chunk;
 }
 
 // One decode row's split attention output before its merge. Chunk c of
@@ -287,7 +295,7 @@ struct SplitRow {
     const float2* ml;
     const float* out;
     const int* pos;
-    int splits, n_heads, head_size;
+    int splits, n_heads, head_size, min_chunk;
 };
 
 // The split merge (cuda_attention.cu:234-255: m = max m_c,

@@ -302,7 +302,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
     }
     if constexpr (MRG) {
         const int n_ctx = *p.att.pos + 1;
-        const int chunk = split_chunk(n_ctx, p.att.splits);
+        const int chunk = split_chunk(n_ctx, p.att.splits, p.att.min_chunk);
         const int n = (n_ctx + chunk - 1) / chunk;
         float v = mout;
         float2 ml8[8];

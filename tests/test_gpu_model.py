@@ -129,15 +129,18 @@ def test_norm_from_producer_sums_of_squares(tmp_path, dim, hidden, heads, kv_hea
 def test_decode_merge_inside_wo_gemv(tmp_path, monkeypatch, dim, hidden, heads, kv_heads,
                                      wtype, seq_len):
     # One-token steps leave the split attention's chunks unmerged, and the wo
-    # GEMV merges them as it stages its A when a row has 2 to 16 chunks of
-    # 64 positions; a row of more (seq_len 2048 allows 32) is merged by the
-    # merge kernel, and the GEMV reads its output. A second model created
-    # with EM_DECODE_MERGE_KERNEL=1 merges every row with the merge kernel
-    # first. Both merge in the same slots and order, so every decode's
-    # logits must be the same bits. The decodes cover one chunk (the split
-    # kernel writes the row itself), a second chunk from position 64, one
-    # slot up to 8 chunks, two from 9 (position 512), 16 from 960 and, at
-    # seq_len 2048, 17 from 1024; each against the CPU Transformer too,
+    # GEMV merges them as it stages its A when a row has 2 to 16 chunks; a
+    # row of more is merged by the merge kernel, and the GEMV reads its
+    # output. A second model created with EM_DECODE_MERGE_KERNEL=1 merges
+    # every row with the merge kernel first. Both merge in the same slots and
+    # order, so every decode's logits must be the same bits. With one head
+    # per split workgroup (hs128) chunks are at least 64 positions: the
+    # decodes cover one chunk (the split kernel writes the row itself), a
+    # second chunk from position 64, one slot up to 8 chunks, two from 9
+    # (position 512), 16 from 960 and, at seq_len 2048, 17 from 1024. With
+    # two heads per workgroup (hs64_gqa) they are at least 32: 2-3 chunks
+    # at 40-80, 16 then 17 at 500-540 (the wo GEMV, then the merge kernel),
+    # 32 from 1000. Each decode is checked against the CPU Transformer too,
     # greedy token equal, within the reference's 1e-4 taken relative to the
     # largest logit (~18 here; the reference's fixture logits are of order
     # 1). The 3e-5 of the short-context test above is too tight over
