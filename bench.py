@@ -731,10 +731,9 @@ def floor_study(em, torch, reps: int = 20) -> dict:
                 (608 MiB, past the Infinity Cache), swept over workgroups,
                 loads in flight per thread and access pattern
       read600   the same sweep as one launch over a 600 MiB buffer (the ceiling)
-      gemv      the int8 GEMV variants of em_probe_gemv_q8 over the headline's
-                38-copy quantised pool: 0 product path (two launches), 1 and 2
-                one launch with the in-kernel arrival, 4 one launch with k split
-                in two halves that meet through an atomic exchange word per output
+      gemv      em_matmul_q8 (skinny) over the headline's 38-copy quantised
+                pool, row-major and unregistered: the split-K GEMV and its slice
+                sum (two launches)
       gemv_packed  em_matmul_q8_packed over the same weights in the strip layout"""
     out = {"method": "HIP-graph replay, HIP events on torch's stream; us per launch"}
     copies = 38
@@ -796,31 +795,16 @@ def floor_study(em, torch, reps: int = 20) -> dict:
     g = torch.Generator(device="cuda")
     g.manual_seed(8)
     A = torch.randn((1, DIM), generator=g, device="cuda", dtype=torch.float32)
-    counters = torch.zeros(DIM // 256, dtype=torch.int32, device="cuda")
     ref = torch.empty((1, DIM), device="cuda")
-    em.probe_gemv_q8(A, pool.ws[0], pool.scales[0], ref, 0)
-    gv = {}
-    for variant in (0, 1, 2, 4):
-        C = torch.zeros((1, DIM), device="cuda")
-        g = graph_of(torch, lambda i, v=variant: em.probe_gemv_q8(
-            A, pool.ws[i % copies], pool.scales[i % copies], C, v, counters), copies)
-        secs, _ = time_graph(torch, g, reps, 3)
-        del g
-        us = secs / (reps * copies) * 1e6
-        row = {"us": round(us, 3), "GBps": round(gemv_bytes(1, DIM, DIM, True) / us / 1e3, 1)}
-        C.zero_()
-        em.probe_gemv_q8(A, pool.ws[0], pool.scales[0], C, variant, counters)
-        C2 = torch.zeros_like(C)
-        em.probe_gemv_q8(A, pool.ws[0], pool.scales[0], C2, variant, counters)
-        torch.cuda.synchronize()
-        row["equal_to_product_path"] = bool(torch.equal(C, ref))
-        row["repeat_identical"] = bool(torch.equal(C, C2))
-        # against |A| x |W| (the tolerance's scale): 1e-4 is the bar
-        bound = (A.abs() @ (pool.ws[0].float().abs() * pool.scales[0])).clamp_min(1e-30)
-        row["max_err_over_abs_bound_vs_product"] = float(((C - ref).abs() / bound).max())
-        gv[str(variant)] = row
-    out["gemv"] = gv
-    out["counters_left_zero"] = bool(torch.count_nonzero(counters).item() == 0)
+    em.matmul(A, pool.ws[0], ref, scale=pool.scales[0], kernel="skinny")
+    C = torch.zeros((1, DIM), device="cuda")
+    g = graph_of(torch, lambda i: em.matmul(A, pool.ws[i % copies], C,
+                                            scale=pool.scales[i % copies], kernel="skinny"),
+                 copies)
+    secs, _ = time_graph(torch, g, reps, 3)
+    del g
+    us = secs / (reps * copies) * 1e6
+    out["gemv"] = {"us": round(us, 3), "GBps": round(gemv_bytes(1, DIM, DIM, True) / us / 1e3, 1)}
     packed = [em.pack_q8(w) for w in pool.ws]
     C = torch.zeros((1, DIM), device="cuda")
     g = graph_of(torch, lambda i: em.matmul_packed(A, packed[i % copies], DIM,
@@ -841,7 +825,7 @@ def floor_study(em, torch, reps: int = 20) -> dict:
     del packed
     del pool
     torch.cuda.synchronize()
-    progress("floor: GEMV variants done")
+    progress("floor: GEMV paths done")
     return out
 
 

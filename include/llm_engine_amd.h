@@ -65,7 +65,9 @@ int em_synchronize(void);
 size_t em_scratch_generation(void);
 
 /* Device memory, for DeviceTensor / DeviceQTensor (cuda_matmul.cu:452-525):
- * allocation, free, and the synchronous copies of upload() / download(). */
+ * allocation, free, and the synchronous copies of upload() / download().
+ * em_free also drops the strip copies registered (em_q8_register) for
+ * buffers inside the freed allocation. */
 int em_malloc(void** ptr, size_t bytes);
 int em_free(void* ptr);
 int em_memcpy_h2d(void* dst, const void* src, size_t bytes);
@@ -127,11 +129,15 @@ int em_unpack_q8(size_t k, size_t n, const int8_t* packed, int8_t* B, void* stre
  * norm weight when n >= 4096) with EM_KERNEL_AUTOMATIC
  * or EM_KERNEL_SKINNY, and, with EM_KERNEL_AUTOMATIC, 2 - 8 rows at
  * k <= 4096 (3 - 4 rows up to n = 24576, 5 - 8 up to n = 4096; A 16-byte
- * aligned). Same
+ * aligned) and 9 - 16 rows where that kernel beats the row-major one (k <=
+ * 768, or k <= 4096 with n <= 12288 and k x n >= 2^24; A, C, scales and the
+ * norm weight 16-byte aligned). Same
  * semantics, results within the same tolerance of the row-major path,
  * bit-identical across repeats. B's bytes must not change while it is
- * registered (register again after changing them); unregister before
- * freeing B. Registering again replaces the copy. Shapes the layout cannot
+ * registered (register again after changing them). Unregister, or free
+ * with em_free (which drops the copy), before the memory is used for other
+ * bytes: a buffer freed another way and allocated again at the same address
+ * would find the stale copy. Registering again replaces the copy. Shapes the layout cannot
  * hold (n % 16 != 0, k % 4 != 0, misaligned B) and EM_STRIP_COPY=0 in the
  * environment leave B unregistered (EM_OK); EM_DECODE_MFMA=0 keeps 2 - 8
  * rows on the row-major kernels. The C++ DeviceQTensor registers its buffer
@@ -144,11 +150,12 @@ int em_q8_unregister(const int8_t* B);
 int em_q8_registered(const int8_t* B, size_t k, size_t n);
 /* C = A x dequantize(B) (C += if accumulate; A replaced by rmsnorm(A) *
  * rms_weight when given), B in the strip layout: the semantics of
- * em_matmul_q8 for m <= 8 rows, in one launch, bit-identical across repeats
- * (the same kernels and bits as a registered em_matmul_q8 call where that
- * runs over the copy). EM_EINVAL for m > 8, n % 16 != 0, k % 4 != 0, a
- * misaligned B, more than 2^31 elements; m == 0 or n == 0 does nothing;
- * k == 0 zeroes C unless accumulating. */
+ * em_matmul_q8 for m <= 16 rows, in one launch, bit-identical across
+ * repeats (the same kernels and bits as a registered em_matmul_q8 call where
+ * that runs over the copy). EM_EINVAL for m > 16, n % 16 != 0, k % 4 != 0, a
+ * misaligned B, more than 2^31 elements, and at 9 to 16 rows for A, C, the
+ * scales or the norm weight off a 16-byte boundary; m == 0 or n == 0 does
+ * nothing; k == 0 zeroes C unless accumulating. */
 int em_matmul_q8_packed(size_t m, size_t n, size_t k, const float* A, const int8_t* packed,
                         const float* scale, float* C, int accumulate, const float* rms_weight,
                         void* stream);
@@ -178,19 +185,10 @@ int em_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream);
  * empty kernel of `blocks` 256-thread workgroups. em_probe_read reads `bytes`
  * at `buf` once with `blocks` workgroups and `depth` (4, 8 or 16) 16-byte
  * loads in flight per thread, each workgroup on one contiguous chunk
- * (contiguous != 0) or the grid striding over the buffer. em_probe_gemv_q8
- * runs one variant of the int8 one-row GEMV (m == 1, n % 16 == 0, 16-byte
- * aligned B): 0 the product path (GEMV, then the slice sum, as em_matmul_q8),
- * 1 one launch whose last workgroup per 256-column tile adds the slices
- * (counters: ceil(n / 256) ints of device memory, zero, left zero), 2 the same
- * with the partials stored as agent-scope atomic stores, 4 one launch with k
- * split in two halves that meet through an atomic exchange word per output
- * (k <= 8192). Every variant writes C. */
+ * (contiguous != 0) or the grid striding over the buffer. */
 int em_probe_empty(unsigned blocks, void* stream);
 int em_probe_read(const void* buf, size_t bytes, uint32_t* sink, unsigned blocks, unsigned depth,
                   int contiguous, void* stream);
-int em_probe_gemv_q8(size_t m, size_t n, size_t k, const float* A, const int8_t* B,
-                     const float* scale, float* C, int variant, int* counters, void* stream);
 
 /* ---- Causal attention over a KV cache (cuda_attention.h) ------------------ */
 

@@ -29,7 +29,7 @@ EXPORTS = (
     "em_last_error", "em_available", "em_synchronize", "em_scratch_generation",
     "em_malloc", "em_free", "em_memcpy_h2d", "em_memcpy_d2h",
     "em_matmul_f32", "em_matmul_q8", "em_matmul_q8_noalloc", "em_quantize_q8", "em_dequantize_q8", "em_stream_read",
-    "em_probe_empty", "em_probe_read", "em_probe_gemv_q8",
+    "em_probe_empty", "em_probe_read",
     "em_pack_q8", "em_unpack_q8", "em_matmul_q8_packed",
     "em_q8_register", "em_q8_unregister", "em_q8_registered",
     "em_attention_check", "em_attention_scratch_floats", "em_attention",
@@ -134,7 +134,6 @@ def lib() -> ctypes.CDLL:
         L.em_q8_registered.argtypes = [_vp, _sz, _sz]
         L.em_probe_empty.argtypes = [ctypes.c_uint, _vp]
         L.em_probe_read.argtypes = [_vp, _sz, _vp, ctypes.c_uint, ctypes.c_uint, ctypes.c_int, _vp]
-        L.em_probe_gemv_q8.argtypes = [_sz, _sz, _sz, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _vp]
         shp = ctypes.POINTER(AttentionShape)
         L.em_attention_check.argtypes = [shp, ctypes.c_int]
         L.em_attention_scratch_floats.argtypes = [shp, _sz, ctypes.c_int]
@@ -315,15 +314,37 @@ def matmul_packed(A, packed, n: int, scale, C=None, *, accumulate=False, rms_wei
     return C
 
 
+# data_ptr -> the finalizer that unregisters it when its tensor is collected.
+_registered: dict = {}
+
+
+def _unregister_ptr(ptr: int) -> None:
+    _registered.pop(ptr, None)
+    if _lib is not None:
+        _lib.em_q8_unregister(ctypes.c_void_p(ptr))
+
+
 def register_q8(q, stream=None) -> None:
     """em_q8_register: the library keeps a strip-layout copy of row-major int8
-    weights q [k, n]; matmul() over q then runs one-row products in one launch."""
+    weights q [k, n]; matmul() over q then runs decode-shaped products in one
+    launch. The registration ends with unregister_q8(q) or when q is
+    collected, whichever comes first, so torch's caching allocator cannot
+    hand q's address to other bytes while a copy of the old ones is kept."""
     import torch
+    import weakref
     k, n = q.shape
-    _check(lib().em_q8_register(_dev(q, torch.int8), k, n, _stream_ptr(stream)))
+    ptr = _dev(q, torch.int8)
+    _check(lib().em_q8_register(ptr, k, n, _stream_ptr(stream)))
+    old = _registered.pop(ptr, None)
+    if old is not None:
+        old.detach()
+    _registered[ptr] = weakref.finalize(q, _unregister_ptr, ptr)
 
 
 def unregister_q8(q) -> None:
+    fin = _registered.pop(q.data_ptr(), None)
+    if fin is not None:
+        fin.detach()
     _check(lib().em_q8_unregister(q.data_ptr()))
 
 
@@ -341,17 +362,6 @@ def probe_read(buf, sink, blocks: int, depth: int, contiguous: bool, stream=None
     """em_probe_read over a device tensor's bytes."""
     _check(lib().em_probe_read(buf.data_ptr(), buf.numel() * buf.element_size(), sink.data_ptr(),
                                blocks, depth, int(bool(contiguous)), _stream_ptr(stream)))
-
-
-def probe_gemv_q8(A, q, scale, C, variant: int, counters=None, stream=None) -> None:
-    """em_probe_gemv_q8: one variant of the int8 one-row GEMV (see the header)."""
-    import torch
-    m, k = A.shape
-    n = q.shape[1]
-    cnt = _dev(counters, torch.int32) if counters is not None else None
-    _check(lib().em_probe_gemv_q8(m, n, k, _dev(A, torch.float32), _dev(q, torch.int8),
-                                  _dev(scale, torch.float32), _dev(C, torch.float32), variant,
-                                  cnt, _stream_ptr(stream)))
 
 
 def dequantize_q8(q, scale, stream=None):

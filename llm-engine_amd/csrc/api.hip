@@ -55,12 +55,51 @@ std::unordered_map<const void*, StripCopy>& strip_copies() {
     return m;
 }
 
-// The strip copy of B if one is registered for this shape, else null.
-const int8_t* strip_copy_of(const void* B, std::size_t k, std::size_t n) {
-    std::lock_guard<std::mutex> lock(g_strip_mu);
+// The strip copy of B if one is registered for this shape, else null. The
+// caller holds g_strip_mu.
+const int8_t* strip_copy_locked(const void* B, std::size_t k, std::size_t n) {
     const auto it = strip_copies().find(B);
     if (it == strip_copies().end() || it->second.k != k || it->second.n != n) return nullptr;
     return it->second.packed;
+}
+
+const int8_t* strip_copy_of(const void* B, std::size_t k, std::size_t n) {
+    std::lock_guard<std::mutex> lock(g_strip_mu);
+    return strip_copy_locked(B, k, n);
+}
+
+// launch(P) with B's strip copy P, if one is registered for this shape; the
+// registry stays locked until launch returns, so no em_q8_unregister or
+// em_free on another thread can free P between the lookup and the launch
+// (they wait for the device before freeing, so the queued kernel finishes
+// first). False, nothing launched, without a copy.
+template <class Launch>
+bool with_strip_copy(const void* B, std::size_t k, std::size_t n, Launch launch) {
+    std::lock_guard<std::mutex> lock(g_strip_mu);
+    const int8_t* P = strip_copy_locked(B, k, n);
+    if (!P) return false;
+    launch(P);
+    return true;
+}
+
+// Frees every strip copy registered for a buffer that starts inside
+// [base, base + bytes). The caller holds g_strip_mu.
+void drop_copies_locked(const char* base, std::size_t bytes) {
+    auto& map = strip_copies();
+    bool synced = false;
+    for (auto it = map.begin(); it != map.end();) {
+        const char* key = static_cast<const char*>(it->first);
+        if (key >= base && key < base + bytes) {
+            if (!synced) {
+                (void)hipDeviceSynchronize();  // a queued product may still read the copy
+                synced = true;
+            }
+            (void)hipFree(it->second.packed);
+            it = map.erase(it);
+        } else {
+            ++it;
+        }
+    }
 }
 
 // One-row products over registered weights run the strip-layout GEMV: one
@@ -158,16 +197,21 @@ int matmul_entry(std::size_t m, std::size_t n, std::size_t k, const float* A, co
         a.stream = s;
         if (std::is_same<BT, int8_t>::value && kernel == EM_KERNEL_SKINNY && m == 1 &&
             strip_row_takes(k, n, rms_weight != nullptr)) {
-            if (const int8_t* P = strip_copy_of(B, k, n)) {
-                run_gemv_packed(a, P);
+            if (with_strip_copy(B, k, n, [&](const int8_t* P) { run_gemv_packed(a, P); })) {
                 hip_check(hipGetLastError(), "launch");
                 return EM_OK;
             }
         }
         if (std::is_same<BT, int8_t>::value && automatic && m >= 2 && decode_mfma_enabled() &&
             decode_mfma_supported(a)) {
-            if (const int8_t* P = strip_copy_of(B, k, n)) {
-                run_decode_mfma(a, P);
+            if (with_strip_copy(B, k, n, [&](const int8_t* P) { run_decode_mfma(a, P); })) {
+                hip_check(hipGetLastError(), "launch");
+                return EM_OK;
+            }
+        }
+        if (std::is_same<BT, int8_t>::value && automatic && strip_split_supported(a) &&
+            strip_split_preferred(a.m, a.n, a.k)) {
+            if (with_strip_copy(B, k, n, [&](const int8_t* P) { run_strip_split(a, P); })) {
                 hip_check(hipGetLastError(), "launch");
                 return EM_OK;
             }
@@ -259,20 +303,20 @@ float* scratch(ScratchSlot slot, std::size_t floats) {
 
 std::size_t scratch_generation() { return g_generation.load(); }
 
-unsigned long long* exchange_words(std::size_t count) {
-    static unsigned long long* words = nullptr;
+unsigned* tile_counters(std::size_t count) {
+    static unsigned* words = nullptr;
     static std::size_t cap = 0;
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (count > cap) {
-        hip_check(hipDeviceSynchronize(), "synchronize before exchange-word growth");
-        if (words) hip_check(hipFree(words), "free exchange words");
+        hip_check(hipDeviceSynchronize(), "synchronize before counter growth");
+        if (words) hip_check(hipFree(words), "free tile counters");
         words = nullptr;
         cap = 0;
         void* p = nullptr;
-        hip_check(hipMalloc(&p, count * sizeof(unsigned long long)), "alloc exchange words");
-        hip_check(hipMemset(p, 0, count * sizeof(unsigned long long)), "clear exchange words");
-        hip_check(hipDeviceSynchronize(), "clear exchange words");
-        words = static_cast<unsigned long long*>(p);
+        hip_check(hipMalloc(&p, count * sizeof(unsigned)), "alloc tile counters");
+        hip_check(hipMemset(p, 0, count * sizeof(unsigned)), "clear tile counters");
+        hip_check(hipDeviceSynchronize(), "clear tile counters");
+        words = static_cast<unsigned*>(p);
         cap = count;
         g_generation.fetch_add(1);
     }
@@ -327,6 +371,20 @@ int em_malloc(void** ptr, size_t bytes) {
 
 int em_free(void* ptr) {
     if (!ptr) return EM_OK;
+    {
+        // Strip copies registered for B inside this allocation go with it:
+        // a later allocation at the same address must not find them.
+        std::lock_guard<std::mutex> lock(em::g_strip_mu);
+        if (!em::strip_copies().empty()) {
+            void* base = nullptr;
+            size_t bytes = 0;
+            if (hipMemGetAddressRange(&base, &bytes, ptr) != hipSuccess || !base) {
+                base = ptr;
+                bytes = 1;
+            }
+            em::drop_copies_locked(static_cast<const char*>(base), bytes);
+        }
+    }
     const hipError_t err = hipFree(ptr);
     if (err != hipSuccess)
         return fail(EM_EDEVICE, std::string("hip: free: ") + hipGetErrorString(err));
@@ -465,7 +523,9 @@ int em_q8_unregister(const int8_t* B) {
     auto& map = em::strip_copies();
     const auto it = map.find(B);
     if (it == map.end()) return EM_OK;
-    const hipError_t err = hipFree(it->second.packed);  // waits for queued work
+    hipError_t err = hipDeviceSynchronize();  // a queued product may still read the copy
+    const hipError_t err2 = hipFree(it->second.packed);
+    if (err == hipSuccess) err = err2;
     map.erase(it);
     if (err != hipSuccess)
         return fail(EM_EDEVICE, std::string("hip: free strip copy: ") + hipGetErrorString(err));
@@ -498,8 +558,8 @@ int em_unpack_q8(size_t k, size_t n, const int8_t* packed, int8_t* B, void* stre
 int em_matmul_q8_packed(size_t m, size_t n, size_t k, const float* A, const int8_t* packed,
                         const float* scale, float* C, int accumulate, const float* rms_weight,
                         void* stream) {
-    if (m > 8)
-        return fail(EM_EINVAL, "matmul_q8_packed: the strip layout takes at most 8 rows " +
+    if (m > 16)
+        return fail(EM_EINVAL, "matmul_q8_packed: the strip layout takes at most 16 rows " +
                                    em::shapes(m, n, k));
     if (too_many(m, k) || too_many(k, n) || too_many(m, n))
         return fail(EM_EINVAL, "matmul_q8_packed: more than 2^31 elements " + em::shapes(m, n, k));
@@ -512,6 +572,13 @@ int em_matmul_q8_packed(size_t m, size_t n, size_t k, const float* A, const int8
         return fail(EM_EINVAL, "matmul_q8_packed: A, B or scale is null " + em::shapes(m, n, k));
     if (k && reinterpret_cast<uintptr_t>(packed) % 16)
         return fail(EM_EINVAL, "matmul_q8_packed: packed B must be 16-byte aligned");
+    auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (m > 8 && k && (!a16(A) || !a16(C) || !a16(scale) || (rms_weight && !a16(rms_weight))))
+        return fail(EM_EINVAL, "matmul_q8_packed: 9 to 16 rows need A, C, the scales and the "
+                               "norm weight 16-byte aligned " + em::shapes(m, n, k));
+    if (m > 8 && n > (size_t{1} << 18))
+        return fail(EM_EINVAL, "matmul_q8_packed: 9 to 16 rows take at most 2^18 columns " +
+                                   em::shapes(m, n, k));
     if (!em::device_present()) return fail(EM_ENODEV, "matmul_q8_packed: no usable GPU");
     hipStream_t s = static_cast<hipStream_t>(stream);
     try {
@@ -529,10 +596,13 @@ int em_matmul_q8_packed(size_t m, size_t n, size_t k, const float* A, const int8
             a.accumulate = accumulate != 0;
             a.rms_weight = rms_weight;
             a.stream = s;
-            if (m >= 2 && em::decode_mfma_enabled() && em::decode_mfma_supported(a))
+            if (m > 8) {
+                em::run_strip_split(a, packed);  // strip_split_supported holds: checked above
+            } else if (m >= 2 && em::decode_mfma_enabled() && em::decode_mfma_supported(a)) {
                 em::run_decode_mfma(a, packed);
-            else
+            } else {
                 em::run_gemv_packed(a, packed);
+            }
         }
         em::hip_check(hipGetLastError(), "launch");
     } catch (const std::exception& e) {
@@ -579,33 +649,6 @@ int em_probe_read(const void* buf, size_t bytes, uint32_t* sink, unsigned blocks
                        contiguous != 0, sink, static_cast<hipStream_t>(stream));
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return fail(EM_EDEVICE, std::string("hip: launch: ") + hipGetErrorString(err));
-    return EM_OK;
-}
-
-int em_probe_gemv_q8(size_t m, size_t n, size_t k, const float* A, const int8_t* B,
-                     const float* scale, float* C, int variant, int* counters, void* stream) {
-    if (m != 1 || n == 0 || k == 0 || too_many(k, n) || n % 16)
-        return fail(EM_EINVAL, "probe_gemv_q8: one row, n a multiple of 16, k > 0");
-    if (!A || !B || !scale || !C || (variant != 0 && !counters))
-        return fail(EM_EINVAL, "probe_gemv_q8: null pointer");
-    if (!em::device_present()) return fail(EM_ENODEV, "probe_gemv_q8: no usable GPU");
-    em::MatmulArgs a{};
-    a.m = 1;
-    a.n = static_cast<int>(n);
-    a.k = static_cast<int>(k);
-    a.A = A;
-    a.B = B;
-    a.scale = scale;
-    a.C = C;
-    a.stream = static_cast<hipStream_t>(stream);
-    try {
-        if (!em::run_skinny_probe(a, variant, counters))
-            return fail(EM_EINVAL, "probe_gemv_q8: variant " + std::to_string(variant) +
-                                       " does not take this shape");
-        em::hip_check(hipGetLastError(), "launch");
-    } catch (const std::exception& e) {
-        return fail(EM_EDEVICE, e.what());
-    }
     return EM_OK;
 }
 

@@ -111,8 +111,6 @@ struct GemvParams {
     const float* ssq;    // NORM 2: sums of squares of A, one per 64 values
     int ssq_parts;       // NORM 2: their count, ceil(k / 64) <= kSsqParts
     SplitRow att;        // merged source: the attention chunks A is merged from
-    float* C;            // ARR: where the last workgroup of a column tile writes C
-    int* arrive;         // ARR: one arrival counter per column tile, 0 between calls
 };
 
 // Where A comes from: read (kSrcA), or formed in the A staging from a
@@ -139,14 +137,7 @@ constexpr int kSsqParts = 4 * kWave;
 // head h's attention chunks (p.att) in the merge kernel's slots and order,
 // so the result is the same as merging first; a row of one chunk, or of
 // more than kMergeInGemv, is read from p.att.out.
-// ARR (k split across workgroups only): 0, the partials are left for a
-// slice sum launched after this kernel. 1 or 2, one launch: every workgroup
-// stores its partials, then counts itself in at its column tile's counter
-// (agent-scope acq_rel, so its stores are visible to whoever counts in
-// last), and the last of the tile's slices adds the slices in order, scales
-// and stores C exactly as reduce_slices does, and resets the counter to 0.
-// 2 also stores the partials as agent-scope atomic stores.
-template <class BT, int MM, int E, int L, int NORM, int SRC = kSrcA, int ARR = 0>
+template <class BT, int MM, int E, int L, int NORM, int SRC = kSrcA>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
     constexpr bool SWI = SRC == kSrcSwiGLU, MRG = SRC == kSrcMerge;
     using LT = Lane<BT, E>;
@@ -471,44 +462,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams<BT> p) {
                 float* o = p.out + static_cast<size_t>(r) * p.n + c;
                 *o = p.accumulate ? *o + v : v;
             } else {
-                float* dst = p.out + (static_cast<size_t>(blockIdx.y) * p.m + r) * p.n + c;
-                if constexpr (ARR == 2) {
-                    __hip_atomic_store(dst, total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                } else {
-                    *dst = total;
-                }
+                p.out[(static_cast<size_t>(blockIdx.y) * p.m + r) * p.n + c] = total;
             }
         }
         if constexpr (E != 16) __syncthreads();
-    }
-    if constexpr (ARR != 0) {
-        // Every store above happens before thread 0's release (the barrier
-        // orders them within the workgroup); the last arrival's acquire then
-        // makes all of the tile's partials visible to its threads.
-        __shared__ int last_s;
-        __syncthreads();
-        if (tid == 0) {
-            const int before = __hip_atomic_fetch_add(p.arrive + blockIdx.x, 1, __ATOMIC_ACQ_REL,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
-            last_s = before == static_cast<int>(gridDim.y) - 1;
-        }
-        __syncthreads();
-        if (last_s) {
-            const uint32_t mn = static_cast<uint32_t>(p.m) * static_cast<uint32_t>(p.n);
-#pragma unroll
-            for (int r = 0; r < MM; ++r) {
-                if (r < p.m && c < p.n) {
-                    const uint32_t i = static_cast<uint32_t>(r * p.n + c);
-                    float total = ordered_sum(p.out, i, mn, static_cast<int>(gridDim.y));
-                    if constexpr (kQ8) total *= p.scale[c];
-                    float* o = p.C + i;
-                    *o = p.accumulate ? *o + total : total;
-                }
-            }
-            if (tid == 0)
-                __hip_atomic_store(p.arrive + blockIdx.x, 0, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        }
     }
 }
 
@@ -779,54 +736,6 @@ void run_skinny(const MatmulArgs& a) {
         run_reduce_slices(a.m, a.n, slices, partial,
                           std::is_same<BT, int8_t>::value ? a.scale : nullptr, a.C,
                           a.accumulate, a.stream);
-}
-
-// Measurement variants of one int8 row at 16 columns per lane (bench.py's
-// floor study): 0 the product path (GEMV, then the slice sum), 1 and 2 one
-// launch with the in-kernel arrival (ARR above; counters: one int per
-// column tile, zero), 4 the one-launch pair GEMV (gemv_pair.hip). False
-// (nothing launched) for any other shape.
-bool run_skinny_probe(const MatmulArgs& a, int variant, int* counters) {
-    const int8_t* B = static_cast<const int8_t*>(a.B);
-    if (a.m != 1 || a.rms_weight || a.n % 16 || !aligned(B, 16) || variant < 0 || variant > 4 ||
-        variant == 3)
-        return false;
-    if (variant == 0) {
-        run_skinny<int8_t>(a);
-        return true;
-    }
-    if (variant == 4) {
-        if (!gemv_pair_supports(a)) return false;
-        run_gemv_pair(a);
-        return true;
-    }
-    const int L = rows_per_lane(16, 1, a.n, a.k);
-    const int slices = ceil_div(a.k, 16 * L);
-    if (slices < 2) return false;
-    GemvParams<int8_t> p{};
-    p.m = 1;
-    p.n = a.n;
-    p.k = a.k;
-    p.A = a.A;
-    p.B = B;
-    p.scale = a.scale;
-    p.direct = 0;
-    p.accumulate = a.accumulate;
-    p.out = scratch(kPartial, static_cast<size_t>(slices) * a.n);
-    p.C = a.C;
-    p.arrive = counters;
-    const dim3 grid(ceil_div(a.n, kThreads), slices);
-    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, a.stream, p); };
-    switch (variant * 100 + L) {
-        case 104: go(gemv_kernel<int8_t, 1, 16, 4, 0, kSrcA, 1>); break;
-        case 108: go(gemv_kernel<int8_t, 1, 16, 8, 0, kSrcA, 1>); break;
-        case 116: go(gemv_kernel<int8_t, 1, 16, 16, 0, kSrcA, 1>); break;
-        case 204: go(gemv_kernel<int8_t, 1, 16, 4, 0, kSrcA, 2>); break;
-        case 208: go(gemv_kernel<int8_t, 1, 16, 8, 0, kSrcA, 2>); break;
-        case 216: go(gemv_kernel<int8_t, 1, 16, 16, 0, kSrcA, 2>); break;
-        default: return false;
-    }
-    return true;
 }
 
 template std::size_t skinny_partial_floats<float>(const MatmulArgs&);

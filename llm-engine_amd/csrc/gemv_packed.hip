@@ -614,7 +614,8 @@ bool gemv_swiglu_supported(const MatmulArgs& a) {
     const int nt = row_threads(a.k);
     const int deepest = nt == 1024 ? 1024 * 4 : nt * 8;
     return a.m == 1 && a.n % (2 * kStrip) == 0 && a.k % 4 == 0 && half > 0 && a.k <= deepest &&
-           reinterpret_cast<uintptr_t>(a.A) % 16 == 0 && !a.accumulate;
+           reinterpret_cast<uintptr_t>(a.A) % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(a.rms_weight) % 16 == 0 && !a.accumulate;
 }
 
 void run_gemv_swiglu(const MatmulArgs& a, const int8_t* packed) {
@@ -664,7 +665,9 @@ void run_gemv_packed(const MatmulArgs& a, const int8_t* packed) {
     p.scale = a.scale;
     p.C = a.C;
     p.accumulate = a.accumulate ? 1 : 0;
-    const bool vec = a.k % 4 == 0 && reinterpret_cast<uintptr_t>(a.A) % 16 == 0;
+    // The float4 kernels load A and the norm weight four values at a time.
+    const bool vec = a.k % 4 == 0 && reinterpret_cast<uintptr_t>(a.A) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(a.rms_weight) % 16 == 0;
     if (a.rms_weight) {
         if (vec) launch_threads<true, true>(p, a.stream);
         else launch_threads<true, false>(p, a.stream);

@@ -34,10 +34,11 @@ enum ScratchSlot { kPartial = 0, kNorm = 1, kQuant = 2, kSplitA = 3, kPartialFro
                    kSlots = 5 };
 float* scratch(ScratchSlot slot, std::size_t floats);
 std::size_t scratch_generation();
-// Library-owned exchange words for the one-launch pair GEMV: `count` 64-bit
-// words, zero. Grow-only like scratch() (growth bumps scratch_generation());
-// zeroed when allocated, and every call leaves the words it used zero.
-unsigned long long* exchange_words(std::size_t count);
+// Library-owned arrival counters for one-launch split-K products: `count`
+// 32-bit words, zero. Grow-only like scratch() (growth bumps
+// scratch_generation()); zeroed when allocated, and every call leaves the
+// counters it used zero.
+unsigned* tile_counters(std::size_t count);
 
 // Compute units of the current device (cached).
 int cu_count();
@@ -171,22 +172,13 @@ void run_fill_zero(float* p, std::size_t count, hipStream_t stream);
 // Reads bytes (a multiple of 16) of buf once, 16-byte aligned.
 void run_stream_read(const void* buf, std::size_t bytes, uint32_t* sink, hipStream_t stream);
 
-// Measurement kernels (probes.hip, gemv.hip): an empty launch of `blocks`
+// Measurement kernels (probes.hip): an empty launch of `blocks`
 // workgroups; one read of `bytes` (a multiple of 16) by `blocks` workgroups
 // with `depth` (4, 8, 16) loads in flight per thread, contiguous chunks per
-// workgroup or a grid stride (false for another depth); and the int8
-// one-row GEMV variants of run_skinny_probe (false for a shape it does not take).
+// workgroup or a grid stride (false for another depth).
 void run_probe_empty(int blocks, hipStream_t stream);
 bool run_probe_read(const void* buf, std::size_t bytes, int blocks, int depth, bool contig,
                     uint32_t* sink, hipStream_t stream);
-bool run_skinny_probe(const MatmulArgs& a, int variant, int* counters);
-
-// One int8 row in one launch (gemv_pair.hip): k split in two halves that
-// meet through an atomic exchange word per output; C (+)= as run_skinny
-// writes it, with the same bits as its two-slice sum. Takes m == 1, no
-// norm, n % 16 == 0, 16-byte aligned B and 2 <= k <= 8192.
-bool gemv_pair_supports(const MatmulArgs& a);
-void run_gemv_pair(const MatmulArgs& a);
 
 // The strip layout of int8 weights (gemv_packed.hip): n / 16 strips of 16
 // columns, strip j holding rows 0 .. k - 1 of columns 16j .. 16j + 15
@@ -208,6 +200,13 @@ const int8_t* registered_strip(const void* B, std::size_t k, std::size_t n);
 // (decode_mfma.hip): n % 16 == 0, k % 4 == 0, k <= 4096, A 16-byte aligned.
 bool decode_mfma_supported(const MatmulArgs& a);
 void run_decode_mfma(const MatmulArgs& a, const int8_t* packed);
+// 9 .. 16 rows over a strip-layout copy, exact bf16 split, k slices added
+// inside the launch (strip_split.hip): n % 16 == 0, k % 4 == 0, A, C,
+// scales and the norm weight 16-byte aligned. strip_split_preferred: where
+// automatic takes it over the row-major exact split for registered weights.
+bool strip_split_supported(const MatmulArgs& a);
+bool strip_split_preferred(int m, int n, int k);
+void run_strip_split(const MatmulArgs& a, const int8_t* packed);
 
 void run_quantize_q8(int rows, int cols, const float* B, int8_t* q, float* scale,
                      hipStream_t stream);

@@ -180,8 +180,13 @@ def test_packed_layout_checks_before_the_gpu():
     assert L.em_pack_q8(4, 16, 8, 16, None) == em.EM_EINVAL
     assert b"16-byte aligned" in L.em_last_error()
     assert L.em_unpack_q8(4, 20, 16, 16, None) == em.EM_EINVAL
-    e = err(lambda: em._check(L.em_matmul_q8_packed(9, 16, 4, 16, 16, 16, 16, 0, None, None)))
-    assert e.code == em.EM_EINVAL and "at most 8 rows" in str(e) and "9x4" in str(e)
+    e = err(lambda: em._check(L.em_matmul_q8_packed(17, 16, 4, 16, 16, 16, 16, 0, None, None)))
+    assert e.code == em.EM_EINVAL and "at most 16 rows" in str(e) and "17x4" in str(e)
+    # 9 to 16 rows (the 16-row strip kernel) need 16-byte A, C, scales, norm weight.
+    e = err(lambda: em._check(L.em_matmul_q8_packed(9, 16, 4, 8, 16, 16, 16, 0, None, None)))
+    assert e.code == em.EM_EINVAL and "16-byte aligned" in str(e) and "9x4" in str(e)
+    e = err(lambda: em._check(L.em_matmul_q8_packed(9, 16, 4, 16, 16, 16, 16, 0, 4, None)))
+    assert e.code == em.EM_EINVAL and "16-byte aligned" in str(e)
     e = err(lambda: em._check(L.em_matmul_q8_packed(1, 20, 4, 16, 16, 16, 16, 0, None, None)))
     assert e.code == em.EM_EINVAL and "multiple of 16" in str(e)
     e = err(lambda: em._check(L.em_matmul_q8_packed(1, 16, 5, 16, 16, 16, 16, 0, None, None)))
@@ -202,8 +207,6 @@ def test_probes_check_before_the_gpu():
     assert L.em_probe_read(16, 64, 16, 256, 5, 0, None) == em.EM_EINVAL
     assert b"depth" in L.em_last_error()
     assert L.em_probe_read(16, 64, 16, 0, 8, 0, None) == em.EM_EINVAL
-    assert L.em_probe_gemv_q8(2, 16, 16, 16, 16, 16, 16, 0, None, None) == em.EM_EINVAL
-    assert L.em_probe_gemv_q8(1, 16, 16, 16, 16, 16, 16, 1, None, None) == em.EM_EINVAL
 
 
 def test_q8_register_checks_before_the_gpu():

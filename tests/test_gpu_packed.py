@@ -277,17 +277,18 @@ def test_registered_decode_rows_against_oracle(shape, fusion):
 
 
 def test_registered_weights_leave_other_calls_row_major():
-    # Explicit kernels, more than 8 rows, k past the strip cut and an
-    # unregistered B all run the row-major kernels: the same bits as before
-    # registering. One row and (automatic) 2 .. 8 rows run over the strip
-    # copy: the same bits as em_matmul_q8_packed, within the tolerance of the
-    # row-major path.
+    # Explicit kernels (12 rows through tiled_split among them), k past the
+    # strip cut and an unregistered B all run the row-major kernels: the same
+    # bits as before registering. One row and (automatic) 2 .. 8 rows run
+    # over the strip copy: the same bits as em_matmul_q8_packed, within the
+    # tolerance of the row-major path (automatic 9 .. 64 rows over the copy:
+    # test_gpu_strip_split.py).
     k, n = 4096, 512
     q, s = em.quantize_q8(dev(inputs.normal((k, n), 0.02, 61)))
     A1 = dev(inputs.normal((1, k), 1.0, 62))
     A4 = dev(inputs.normal((4, k), 1.0, 63))
     A12 = dev(inputs.normal((12, k), 1.0, 66))
-    same = (("m4 skinny", A4, "skinny"), ("m12", A12, "automatic"), ("tiled", A1, "tiled"),
+    same = (("m4 skinny", A4, "skinny"), ("m12 tiled_split", A12, "tiled_split"), ("tiled", A1, "tiled"),
             ("naive", A1, "naive"))
     before = {name: host(em.matmul(A, q, scale=s, kernel=kern)).copy() for name, A, kern in same}
     row = {m: host(em.matmul(A, q, scale=s)).copy() for m, A in ((1, A1), (4, A4))}
@@ -357,3 +358,97 @@ def test_registered_graph_replay_matches_eager():
         torch.cuda.synchronize()
     finally:
         em.unregister_q8(q)
+
+
+def _q8_product_raw(B_ptr, A, s, k, n):
+    C = torch.empty((A.shape[0], n), device="cuda")
+    em.matmul_q8_raw(A.shape[0], n, k, A.data_ptr(), B_ptr, s.data_ptr(), C.data_ptr())
+    return host(C)
+
+
+def test_em_free_drops_the_registration():
+    # A registered buffer freed with em_free takes its strip copy with it:
+    # a new allocation at the same address, holding other bytes, must not be
+    # multiplied by the stale copy (the reference's DeviceQTensor owns and
+    # frees its bytes, cuda_matmul.cu:488-513, so it has no copy to go stale).
+    import ctypes
+    L = em.lib()
+    k, n = 1024, 256
+    qa, s = orc.quantize_q8(inputs.normal((k, n), 0.02, 301))
+    qb, _ = orc.quantize_q8(inputs.normal((k, n), 0.02, 302))
+    A = dev(inputs.normal((1, k), 1.0, 303))
+    sd = dev(s)
+    p1 = ctypes.c_void_p()
+    assert L.em_malloc(ctypes.byref(p1), k * n) == em.EM_OK
+    assert L.em_memcpy_h2d(p1, qa.ctypes.data, k * n) == em.EM_OK
+    assert L.em_q8_register(p1, k, n, None) == em.EM_OK
+    assert L.em_q8_registered(p1, k, n) == 1
+    first = _q8_product_raw(p1.value, A, sd, k, n)
+    assert L.em_free(p1) == em.EM_OK
+    assert L.em_q8_registered(p1, k, n) == 0
+    p2 = ctypes.c_void_p()
+    assert L.em_malloc(ctypes.byref(p2), k * n) == em.EM_OK
+    try:
+        assert L.em_memcpy_h2d(p2, qb.ctypes.data, k * n) == em.EM_OK
+        got = _q8_product_raw(p2.value, A, sd, k, n)
+        check(got, orc.matmul_fused(host(A), Bq=qb, scale=s), host(A), orc.dequantize(qb, s), k)
+        check(first, orc.matmul_fused(host(A), Bq=qa, scale=s), host(A), orc.dequantize(qa, s), k)
+        if p2.value != p1.value:
+            pytest.skip("the second allocation got another address; the copy was dropped anyway")
+    finally:
+        L.em_free(p2)
+
+
+def test_python_registration_ends_with_its_tensor():
+    # register_q8 ties the registration to the tensor: once it is collected,
+    # torch's caching allocator may hand the same address to new bytes, which
+    # must be multiplied as they are.
+    import gc
+    k, n = 2048, 512
+    qa, s = orc.quantize_q8(inputs.normal((k, n), 0.02, 311))
+    qb, _ = orc.quantize_q8(inputs.normal((k, n), 0.02, 312))
+    A = dev(inputs.normal((1, k), 1.0, 313))
+    sd = dev(s)
+    q = dev(qa)
+    addr = q.data_ptr()
+    em.register_q8(q)
+    assert em.registered_q8(q)
+    del q
+    gc.collect()
+    torch.cuda.synchronize()
+    q2 = dev(qb)
+    assert not em.registered_q8(q2)
+    got = host(em.matmul(A, q2, scale=sd))
+    check(got, orc.matmul_fused(host(A), Bq=qb, scale=s), host(A), orc.dequantize(qb, s), k)
+    if q2.data_ptr() != addr:
+        pytest.skip("the caching allocator gave another address; the registration ended anyway")
+
+
+@pytest.mark.parametrize("m", [1, 12])
+@pytest.mark.parametrize("shape", [(4096, 4096), (288, 864)], ids=lambda s: "x".join(map(str, s)))
+def test_registered_misaligned_norm_weight(shape, m):
+    # The norm weight one float past a 16-byte boundary (the reference's
+    # MatmulFusion.rms_weight may be any device float pointer,
+    # cuda_matmul.h:85-92): the kernels that load it four floats at a time
+    # are passed over for ones that load it per value; within the oracle's
+    # bound, the same bits on a second call.
+    k, n = shape
+    A = inputs.uniform((m, k), -1.0, 1.0, 321)
+    q, s = orc.quantize_q8(inputs.normal((k, n), 0.02, 322))
+    w = inputs.uniform((k,), 0.5, 1.5, 323)
+    qd, sd = dev(q), dev(s)
+    wbuf = torch.zeros((k + 1,), device="cuda")
+    wbuf[1:] = dev(w)
+    wm = wbuf[1:]
+    assert wm.data_ptr() % 16 == 4
+    em.register_q8(qd)
+    try:
+        C = torch.empty((m, n), device="cuda")
+        em.matmul(dev(A), qd, C, scale=sd, rms_weight=wm)
+        got = host(C).copy()
+        em.matmul(dev(A), qd, C, scale=sd, rms_weight=wm)
+        assert np.array_equal(got, host(C))
+    finally:
+        em.unregister_q8(qd)
+    want = orc.matmul_fused(A, Bq=q, scale=s, w=w)
+    check(got, want, orc.rmsnorm(A, w), orc.dequantize(q, s), k, 2.0)
