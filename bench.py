@@ -428,6 +428,49 @@ def checkpoint_load_case(em, torch) -> dict:
     return out
 
 
+def fp32_decode_table(em, torch, steps: int, ms=(1, 4, 8, 16, 32, 64)) -> dict:
+    """The reference bench's fp32 decode table (bench_cuda.cpp:112-144: m x
+    4096^2, the engine beside cuBLAS and beside the engine with its copies)
+    on this build: em_matmul_f32 (automatic) over the rotating >600 MiB fp32
+    pool, graph replay; torch.mm (the vendor GEMM) over the same pool by the
+    same method; and the reference's "with copies" convention, host time of
+    upload A (pageable) -> product -> download C, one resident W, median of
+    101."""
+    out = {}
+    for m in ms:
+        r, _ = gemv_case(em, torch, m, False, max(5, steps // 2), 2)
+        pool = Pool(em, torch, False, DIM, DIM, r["copies"], 1000)
+        g = torch.Generator(device="cuda")
+        g.manual_seed(7 + m)
+        A = torch.randn((m, DIM), generator=g, device="cuda", dtype=torch.float32)
+        C = torch.empty((m, DIM), device="cuda")
+        graph = graph_of(torch, lambda i: torch.mm(A, pool.ws[i % len(pool.ws)], out=C),
+                         len(pool.ws))
+        secs, _ = time_graph(torch, graph, max(5, steps // 2), 2)
+        vendor_us = secs / (max(5, steps // 2) * len(pool.ws)) * 1e6
+        del graph
+        W = pool.ws[0]
+        A_host = A.cpu()
+        C_host = torch.empty((m, DIM), dtype=torch.float32)
+        times = []
+        for i in range(102):
+            t0 = time.perf_counter()
+            A.copy_(A_host)
+            em.matmul(A, W, C)
+            C_host.copy_(C)
+            torch.cuda.synchronize()
+            if i:
+                times.append(time.perf_counter() - t0)
+        pool.close()
+        del pool
+        times.sort()
+        out[f"m{m}"] = {"us": round(r["us_per_call"], 3), "GBps": round(r["GBps"], 1),
+                        "pct_of_hbm_peak": round(100 * r["GBps"] / HBM_PEAK_GBS, 1),
+                        "torch_mm_us": round(vendor_us, 3),
+                        "with_copies_us": round(times[len(times) // 2] * 1e6, 1)}
+    return out
+
+
 def host_median_convention(em, torch, A, w, s, C, reps=101):
     """The reference's bench_cuda convention: host time launch -> synchronize."""
     em.matmul(A, w, C, scale=s)
@@ -1061,9 +1104,10 @@ def main() -> int:
                                         "pct_of_roofline": round(100 * max(t_mfma, t_hbm) * 1e6 / r["us_per_call"], 1),
                                         "unregistered_rowmajor_us": round(rr["us_per_call"], 3),
                                         "unregistered_kernel": q8_kernel(m)[0]}
-        r, _ = gemv_case(em, torch, 1, False, max(5, steps // 2), 2)
-        extra["fp32_gemv_m1"] = {"us": round(r["us_per_call"], 3), "GBps": round(r["GBps"], 1),
-                                 "pct_of_hbm_peak": round(100 * r["GBps"] / HBM_PEAK_GBS, 1)}
+        extra["fp32_decode_4096"] = fp32_decode_table(em, torch, steps)
+        extra["fp32_gemv_m1"] = {k: extra["fp32_decode_4096"]["m1"][k]
+                                 for k in ("us", "GBps", "pct_of_hbm_peak")}
+        progress("fp32 decode table done")
         gemm, gemm_AB = gemm_case(em, torch)
         extra["fp32_gemm_N4096"] = {k: round(v, 3) if isinstance(v, float) else v
                                     for k, v in gemm.items()}

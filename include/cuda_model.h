@@ -16,6 +16,7 @@
 #pragma once
 
 #include <cstddef>
+#include <memory>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -52,13 +53,16 @@ public:
     // the reference's loader rejects, with its message. Not in the
     // reference's class.
     static CudaTransformer load(const std::string& path, WeightType type = WeightType::f32) {
-        em_model* m = nullptr;
-        const int rc =
-            em_model_load(path.c_str(), type == WeightType::q8 ? EM_WEIGHTS_Q8 : EM_WEIGHTS_F32, &m);
+        em_model* raw = nullptr;
+        const int rc = em_model_load(path.c_str(),
+                                     type == WeightType::q8 ? EM_WEIGHTS_Q8 : EM_WEIGHTS_F32, &raw);
         if (rc == EM_EINVAL) throw std::invalid_argument(em_last_error());
         if (rc != EM_OK) throw std::runtime_error(em_last_error());
+        // Owned here until the CudaTransformer holds it, so a throwing
+        // constructor (the logits' allocation) does not leak the model.
+        std::unique_ptr<em_model, int (*)(em_model*)> m(raw, em_model_destroy);
         em_model_config c{};
-        em_model_config_get(m, &c);
+        em_model_config_get(m.get(), &c);
         Config cfg{};
         cfg.dim = c.dim;
         cfg.hidden_dim = c.hidden_dim;
@@ -67,7 +71,9 @@ public:
         cfg.n_kv_heads = c.n_kv_heads;
         cfg.vocab_size = c.vocab_size;
         cfg.seq_len = c.seq_len;
-        return CudaTransformer(m, cfg);
+        CudaTransformer t(m.get(), cfg);
+        m.release();
+        return t;
     }
     CudaTransformer(CudaTransformer&& o) noexcept
         : cfg_(o.cfg_), m_(o.m_), logits_(std::move(o.logits_)) {

@@ -223,16 +223,8 @@ int decode_groups(int m) { return m <= 4 ? 1 : 2; }
 
 // Threads per workgroup: 1024 (four waves per SIMD, so one wave's MFMAs
 // run while another waits for its weights: 4096^2 at m = 4 took 7.8 us at
-// 256 threads, 6.3 at 1024); EM_DECODE_THREADS (256, 512) overrides it for
-// tuning sweeps.
-int decode_threads() {
-    static const int nt = [] {
-        const char* v = std::getenv("EM_DECODE_THREADS");
-        const int x = v ? std::atoi(v) : 0;
-        return x == 256 || x == 512 ? x : 1024;
-    }();
-    return nt;
-}
+// 256 threads, 6.3 at 1024).
+constexpr int kDecodeThreads = 1024;
 
 template <int NT, int G, int R, bool NORM, bool EXACT>
 void launch_decode(const DecodeParams& p, hipStream_t s) {
@@ -268,11 +260,7 @@ void launch_decode_rounds(DecodeParams p, hipStream_t s) {
 
 template <int G, bool NORM>
 void launch_decode_threads(const DecodeParams& p, hipStream_t s) {
-    switch (decode_threads()) {
-        case 256: return launch_decode_rounds<256, G, NORM>(p, s);
-        case 512: return launch_decode_rounds<512, G, NORM>(p, s);
-        default: return launch_decode_rounds<1024, G, NORM>(p, s);
-    }
+    launch_decode_rounds<kDecodeThreads, G, NORM>(p, s);
 }
 
 }  // namespace

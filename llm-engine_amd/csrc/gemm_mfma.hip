@@ -469,14 +469,9 @@ bool vec_ok(const MatmulArgs& a, size_t b_align) {
 
 // The streamlined kernel's conditions: fp32 B, whole 32-deep k steps, rows of
 // whole float4s, 16-byte aligned operands, and per-tile offsets within the
-// buffer descriptors' 31-bit range. EM_TILED_FAST=0 keeps every product on
-// gemm_tiled_kernel (A/B comparisons).
+// buffer descriptors' 31-bit range.
 bool fast_ok(const MatmulArgs& a) {
-    static const bool enabled = [] {
-        const char* v = std::getenv("EM_TILED_FAST");
-        return !(v && v[0] == '0');
-    }();
-    return enabled && a.k % FK == 0 && a.n % 4 == 0 &&
+    return a.k % FK == 0 && a.n % 4 == 0 &&
            reinterpret_cast<uintptr_t>(a.A) % 16 == 0 &&
            reinterpret_cast<uintptr_t>(a.B) % 16 == 0 &&
            reinterpret_cast<uintptr_t>(a.C) % 16 == 0 &&
@@ -520,23 +515,8 @@ void launch_fast(const MatmulArgs& a, int per_cu) {
 // workgroups share a CU and cover each other's barriers and loads, which
 // measured faster than 128 x 128 tiles at every size tried (fp32 N = 1024 /
 // 2048 / 4096: 97.6 / 133.1 / 143.9 against 66.9 / 123.7 / 142.9 TFLOP/s).
-// EM_TILED_TILE=128 selects the larger tile (tuning comparisons).
-void run_fast(const MatmulArgs& a) {
-    static const int per_cu = [] {
-        const char* v = std::getenv("EM_TILED_BLOCKS_PER_CU");
-        const int x = v ? std::atoi(v) : 0;
-        return x > 0 ? x : 1;
-    }();
-    static const bool big = [] {
-        const char* v = std::getenv("EM_TILED_TILE");
-        return v && std::atoi(v) == 128;
-    }();
-    if (big) {
-        launch_fast<4>(a, per_cu);
-    } else {
-        launch_fast<2>(a, per_cu);
-    }
-}
+// k is split until the grid holds one workgroup per CU.
+void run_fast(const MatmulArgs& a) { launch_fast<2>(a, 1); }
 
 bool tiled_preferred(const MatmulArgs& a) {
     if (a.m <= 8 || !fast_ok(a)) return false;
@@ -555,12 +535,8 @@ void run_tiled(const MatmulArgs& a) {
     // Split k when the tile grid gives fewer than two workgroups per CU and
     // k is deep enough for each slice to keep 256+ rows (two per CU measured
     // 1.2-1.3x faster than one on the Llama-7B m = 512 projections, and four
-    // no better). EM_TILED_BLOCKS_PER_CU overrides the target (tuning sweeps).
-    static const int per_cu = [] {
-        const char* v = std::getenv("EM_TILED_BLOCKS_PER_CU");
-        const int x = v ? std::atoi(v) : 0;
-        return x > 0 ? x : 2;
-    }();
+    // no better).
+    constexpr int per_cu = 2;
     int slices = 1;
     const long long target = static_cast<long long>(per_cu) * cu_count();
     if (tiles < target) {

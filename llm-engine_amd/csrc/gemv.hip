@@ -528,14 +528,9 @@ bool aligned(const void* ptr, size_t bytes) {
 // nontemporal weight loads one 16-row-deep workgroup per CU streams a
 // 4096^2 int8 matrix faster than two 8-deep ones, and sweeps over the
 // Llama-7B and stories15M shapes put the cut near CUs / 2.
-// EM_GEMV_ROWS_PER_LANE overrides it (tuning sweeps).
 // The result is what the launched kernel uses: capped by max_depth as
 // pick_rows caps it.
 int rows_per_lane(int E, int m, int n, int k) {
-    static const int forced = [] {
-        const char* v = std::getenv("EM_GEMV_ROWS_PER_LANE");
-        return v ? std::atoi(v) : 0;
-    }();
     if (E == 1) return 16;
     const int mm = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
     const int cap = max_depth(E, mm);
@@ -543,9 +538,7 @@ int rows_per_lane(int E, int m, int n, int k) {
     // take 8 rows (4 would make 16-row slices, 18 of them at k = 288: the
     // stories15M fp32 decode ran 0.217 ms/token against 0.198 at 8).
     int L = E == 4 ? 8 : 4;
-    if (forced == 4 || forced == 8 || forced == 16 || forced == 32) {
-        L = forced;
-    } else if (k <= E * cap && ceil_div(n, kThreads) >= cu_count() / 4) {
+    if (k <= E * cap && ceil_div(n, kThreads) >= cu_count() / 4) {
         // All of k in one slice when the columns alone give a quarter of a
         // workgroup per CU: no partials and no second launch (the stories15M
         // classifier, k = 288, n = 32000). Narrower products still split k,

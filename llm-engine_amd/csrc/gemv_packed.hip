@@ -465,17 +465,6 @@ __global__ __launch_bounds__(NT) void gemv_row_kernel(PackedParams p) {
     }
 }
 
-// Threads per workgroup: 256 by default; EM_PACKED_THREADS (256, 512 or
-// 1024) overrides it for tuning sweeps.
-int packed_threads() {
-    static const int nt = [] {
-        const char* v = std::getenv("EM_PACKED_THREADS");
-        const int x = v ? std::atoi(v) : 0;
-        return x == 512 || x == 1024 ? x : 256;
-    }();
-    return nt;
-}
-
 // Rows per lane L for MM rows of A: capped at LMAX (more rows of A hold
 // more accumulators and A values per lane). One batch holds NT x L rows.
 template <int NT, int MM, bool NORM, bool VEC, int LMAX>
@@ -546,53 +535,28 @@ bool launch_row(const PackedParams& p, hipStream_t s) {
     return true;
 }
 
-// Threads per workgroup of gemv_row_kernel: EM_PACKED_THREADS (256, 512 or
-// 1024) when set, else 512 above 2048 rows of k and 256 up to it.
-int row_threads(int k) {
-    static const int env = [] {
-        const char* v = std::getenv("EM_PACKED_THREADS");
-        const int x = v ? std::atoi(v) : 0;
-        return x == 256 || x == 512 || x == 1024 ? x : 0;
-    }();
-    return env ? env : k > 2048 ? 512 : 256;
-}
-
-// EM_PACKED_ROW=0 sends one-row products back to gemv_packed_kernel (A
-// staged in LDS), for comparisons.
-bool row_kernel_enabled() {
-    static const bool on = [] {
-        const char* v = std::getenv("EM_PACKED_ROW");
-        return !(v && std::string(v) == "0");
-    }();
-    return on;
-}
+// Threads per workgroup of gemv_row_kernel: 512 above 2048 rows of k and
+// 256 up to it.
+int row_threads(int k) { return k > 2048 ? 512 : 256; }
 
 template <bool NORM, bool VEC>
 void launch_threads(const PackedParams& p, hipStream_t s) {
-    if (p.m == 1 && VEC && row_kernel_enabled()) {
+    if (p.m == 1 && VEC) {
         // 512 threads (two waves per SIMD, one multiplying while the other
         // waits for its loads) above 2048 rows of k, 256 up to it (4096^2:
         // 4.7 against 4.9 us; 2048 x 8192: 4.8 against 4.7); at most 4096
-        // rows at 256 threads (1024 by request), 8192 at 512 (12288 without
-        // a norm). Deeper k loops in gemv_packed_kernel.
+        // rows at 256 threads, 8192 at 512 (12288 without a norm). Deeper k
+        // loops in gemv_packed_kernel.
         const int nt = row_threads(p.k);
-        if (nt == 1024 && launch_row<1024, NORM>(p, s)) return;
         if (nt == 256 && launch_row<256, NORM>(p, s)) return;
         if (launch_row<512, NORM>(p, s)) return;
     }
     if (p.m <= 1) {
         // Past 8192 rows a 256-thread workgroup would loop over batches;
         // 512 threads hold up to 16384 rows in one batch.
-        if (p.k > kThreads * 32 && p.k <= 512 * 32 && packed_threads() == 256)
+        if (p.k > kThreads * 32 && p.k <= 512 * 32)
             return launch_depth<512, 1, NORM, VEC, 32>(packed_depth(512, p.k, 32), p, s);
-        switch (packed_threads()) {
-            case 1024:
-                return launch_depth<1024, 1, NORM, VEC, 8>(packed_depth(1024, p.k, 8), p, s);
-            case 512:
-                return launch_depth<512, 1, NORM, VEC, 16>(packed_depth(512, p.k, 16), p, s);
-            default:
-                return launch_depth<256, 1, NORM, VEC, 32>(packed_depth(256, p.k, 32), p, s);
-        }
+        return launch_depth<256, 1, NORM, VEC, 32>(packed_depth(256, p.k, 32), p, s);
     }
     if (p.m <= 2) return launch_depth<256, 2, NORM, VEC, 16>(packed_depth(256, p.k, 16), p, s);
     if (p.m <= 4) return launch_depth<256, 4, NORM, VEC, 8>(packed_depth(256, p.k, 8), p, s);

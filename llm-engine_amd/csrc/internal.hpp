@@ -149,8 +149,7 @@ struct RopeFuse {
 // rope_cache_kernel's arithmetic; returns true. Otherwise C as usual, false.
 bool run_split_bf16(const MatmulArgs& a, const RopeFuse* rope = nullptr);
 // True if automatic sends an int8 product of m rows (k x n weights) to the
-// exact-split kernel rather than the GEMV. EM_SPLIT_MIN_ROWS (2 or more)
-// replaces the rule by a row threshold, for sweeps.
+// exact-split kernel rather than the GEMV.
 bool split_bf16_preferred(int m, int n, int k);
 
 // True if run_tiled_split can take this shape (vector loads of B rows).

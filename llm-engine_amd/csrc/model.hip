@@ -514,7 +514,28 @@ public:
     // An (out x in) row-major matrix, transposed into columns col0 .. col0 +
     // out of dst (in x ld): read_transposed, model.cpp:43-53.
     void transposed(std::size_t out, std::size_t in, float* dst, std::size_t ld, std::size_t col0) {
-        const std::size_t rows_per = std::max<std::size_t>(1, kChunk / sizeof(float) / in);
+        const std::size_t per = kChunk / sizeof(float);
+        if (in > per) {
+            // A row longer than a chunk (a wide w2): each row in chunk-sized
+            // segments, segment [c, c + len) landing in rows c .. c + len - 1
+            // of dst, column col0 + r.
+            for (std::size_t r = 0; r < out; ++r) {
+                for (std::size_t c = 0; c < in; c += per) {
+                    const std::size_t len = std::min(per, in - c);
+                    float* h = next(len);
+                    float* d = dev_[cur_];
+                    check(hipMemcpyAsync(d, h, len * sizeof(float), hipMemcpyHostToDevice, s_),
+                          "upload checkpoint");
+                    const dim3 grid(ceil_div(static_cast<long long>(len), 32), 1);
+                    hipLaunchKernelGGL(transpose_kernel, grid, dim3(kThreads), 0, s_, d,
+                                       std::size_t{1}, len, dst + c * ld, ld, col0 + r);
+                    check(hipGetLastError(), "launch");
+                    check(hipEventRecord(done_[cur_], s_), "event");
+                }
+            }
+            return;
+        }
+        const std::size_t rows_per = per / in;
         for (std::size_t r = 0; r < out; r += rows_per) {
             const std::size_t rows = std::min(rows_per, out - r);
             float* h = next(rows * in);

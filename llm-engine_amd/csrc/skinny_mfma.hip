@@ -330,11 +330,7 @@ void run_tiled_split(const MatmulArgs& a) {
     p.out = p.direct ? a.C : scratch(kPartial, static_cast<size_t>(slices) * a.m * a.n);
     p.row_tiles = row_tiles;
     p.col_tiles = col_tiles;
-    static const int xcd_env = [] {
-        const char* v = std::getenv("EM_XCD_ORDER");
-        return v ? std::atoi(v) : 1;
-    }();
-    p.xcd_order = xcd_env;
+    p.xcd_order = 1;
     const dim3 grid(col_tiles * slices * row_tiles);
     const bool avec = a.k % 4 == 0 && reinterpret_cast<uintptr_t>(a.A) % 16 == 0;
     if (RB == 1) {

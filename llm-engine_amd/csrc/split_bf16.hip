@@ -671,22 +671,11 @@ bool split_bf16_supports(const MatmulArgs& a) {
 // So: from 5 rows always; from 3 rows for 2^25 weights or more; from 2 rows
 // for 2^26 or more.
 bool split_bf16_preferred(int m, int n, int k) {
-    static const int forced = [] {
-        const char* v = std::getenv("EM_SPLIT_MIN_ROWS");  // tuning sweeps
-        const int x = v ? std::atoi(v) : 0;
-        return x >= 2 ? x : 0;
-    }();
-    if (forced) return m >= forced;
     const long long w = static_cast<long long>(n) * k;
     return m >= 5 || (m >= 3 && w >= (1LL << 25)) || (m >= 2 && w >= (1LL << 26));
 }
 
 bool run_split_bf16(const MatmulArgs& a, const RopeFuse* rope) {
-    static const int forced_rb = [] {
-        const char* v = std::getenv("EM_SPLIT_ROW_BLOCKS");
-        const int x = v ? std::atoi(v) : 0;
-        return x == 1 || x == 2 || x == 4 ? x : 0;
-    }();
     // Without a norm, the kernel splits A itself, chunk by chunk (needs whole
     // 8-value groups and 16-byte rows); otherwise a pre-pass writes the three
     // planes with the norm fused.
@@ -714,7 +703,7 @@ bool run_split_bf16(const MatmulArgs& a, const RopeFuse* rope) {
         const double rounds = grid / cu_count();
         return rounds <= 1.0 || rounds / std::ceil(rounds) >= (raw ? 0.8 : 0.7);
     };
-    const int RB = forced_rb ? forced_rb : fits(4) ? 4 : fits(2) ? 2 : 1;
+    const int RB = fits(4) ? 4 : fits(2) ? 2 : 1;
     const int row_tiles = ceil_div(a.m, 16 * RB);
     const int m_pad = row_tiles * 16 * RB;
     const int k_pad = ceil_div(a.k, kChunk) * kChunk;
@@ -788,7 +777,7 @@ bool run_split_bf16(const MatmulArgs& a, const RopeFuse* rope) {
     // bits. qkv of a 512-row Llama-7B prefill: 384 tiles, 128 of them the
     // last round.
     int tail_cols = 0;
-    if (RB == 4 && slices == 1 && !forced_rb) {
+    if (RB == 4 && slices == 1) {
         const long long cu = cu_count();
         const long long full = blocks / cu * cu, rest = blocks - full;
         if (full > 0 && rest > 0 && 2 * rest <= cu && full % row_tiles == 0)

@@ -9,6 +9,12 @@ oracle/Makefile's e2e target (the built binaries travel in oracle/_ref):
                                  Transformer (model.cpp)
   oracle/_ref/bench_matmul_gpu   bench/bench_matmul.cpp on this build's
                                  matmul.h / quant.h (the GPU entry points)
+  oracle/_ref/test_matmul_gpu    tests/test_matmul.cpp on the same headers:
+                                 the known answer, 17 edge shapes at 1e-5 k,
+                                 thread counts, the "2x3"/"4x2" message
+  oracle/_ref/test_quant_gpu     tests/test_quant.cpp on the same headers:
+                                 quantize_q8 / dequantize round trip and the
+                                 int8 products against the dequantized ones
 The reference's cuda_attention test and bench_cuda include the CUDA runtime
 and cuBLAS directly, so they cannot be built here; tests/test_gpu_attention.py
 covers attention. Exit 77 means no GPU (skip), as in the reference's CTest
@@ -25,6 +31,12 @@ SUITES = {
     "model": os.path.join(REF_BIN, "test_cuda_model"),
 }
 BENCH = os.path.join(REF_BIN, "bench_matmul_gpu")
+# The reference's CPU-entry-point tests (no GPU check of their own: run on
+# the GPU box only).
+CPU_ENTRY = {
+    "matmul": os.path.join(REF_BIN, "test_matmul_gpu"),
+    "quant": os.path.join(REF_BIN, "test_quant_gpu"),
+}
 
 
 def run(path, *args, timeout=900):
@@ -43,9 +55,23 @@ def test_reference_suite_links_and_skips_without_gpu(which):
     assert "skipping" in r.stdout
 
 
-def test_reference_bench_links():
-    out = subprocess.run(["ldd", BENCH], capture_output=True, text=True).stdout
+@pytest.mark.parametrize("path", [BENCH] + [CPU_ENTRY[k] for k in sorted(CPU_ENTRY)],
+                         ids=["bench_matmul"] + sorted(CPU_ENTRY))
+def test_reference_cpu_entry_programs_link(path):
+    if not os.path.exists(path):
+        pytest.fail(f"{path} is not built (__graft_entry__.build())")
+    out = subprocess.run(["ldd", path], capture_output=True, text=True).stdout
     assert "libllm_engine_amd.so" in out, out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("which", sorted(CPU_ENTRY))
+def test_reference_cpu_entry_tests_on_the_gpu(which):
+    # matmul_naive / blocked / parallel and quantize_q8 / dequantize with the
+    # reference's signatures, each call on the MI355X.
+    r = run(CPU_ENTRY[which], timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "all tests passed" in r.stdout
 
 
 @pytest.mark.gpu

@@ -98,3 +98,45 @@ def test_large_sections_cross_staging_chunks(tmp_path):
     loaded = em.Model.load(path, q8=True)
     check_arrays(loaded, ck, True)
     loaded.close()
+
+
+def test_load_rows_longer_than_a_staging_chunk(tmp_path):
+    # w2 is stored dim rows of hidden_dim floats; with hidden_dim past 2^24
+    # one row is longer than the loader's 64 MiB staging chunk, so rows go in
+    # segments. A sparse file (zeros but for planted values at the segment
+    # edges) must land transposed, every planted value in its place and
+    # nothing else non-zero (the reference's read_transposed,
+    # model.cpp:43-53, reads a row at a time into a buffer of its size).
+    dim, heads, vocab, seq_len = 16, 4, 8, 8
+    per = (64 << 20) // 4
+    H = per + 48
+    header = np.array([dim, H, 1, heads, heads, vocab, seq_len], np.int32)
+    path = str(tmp_path / "wide.bin")
+    off = header.nbytes
+    sizes = [("emb", vocab * dim), ("rms_att", dim), ("wq", dim * dim), ("wk", dim * dim),
+             ("wv", dim * dim), ("wo", dim * dim), ("rms_ffn", dim), ("w1", H * dim),
+             ("w2", dim * H), ("w3", H * dim), ("rms_final", dim), ("freq", seq_len * dim // heads)]
+    at = {}
+    for name, count in sizes:
+        at[name] = off
+        off += 4 * count
+    plants = {}  # (row of w2 in the file, column) -> value
+    for r in (0, 7, dim - 1):
+        for c in (0, per - 1, per, per + 1, H - 1):
+            plants[(r, c)] = np.float32(1.0 + r + c * 1e-7)
+    with open(path, "wb") as f:
+        f.write(header.tobytes())
+        f.seek(off - 4)
+        f.write(np.zeros(1, np.float32).tobytes())
+        for (r, c), v in plants.items():
+            f.seek(at["w2"] + 4 * (r * H + c))
+            f.write(np.array([v], np.float32).tobytes())
+    model = em.Model.load(path, q8=False)
+    try:
+        w2 = model.weight("w2")  # H x dim: the file's w2 transposed
+        assert w2.shape == (H, dim)
+        for (r, c), v in plants.items():
+            assert w2[c, r] == v, (r, c)
+        assert int(np.count_nonzero(w2)) == len(plants)
+    finally:
+        model.close()
