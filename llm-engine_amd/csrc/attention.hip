@@ -89,11 +89,17 @@ int split_lanes(const AttnShape& s) {
 }
 int split_f(const AttnShape& s) { return (s.head_size / 4 + split_lanes(s) - 1) / split_lanes(s); }
 
-// Slot merge buffers, plus with RoPE fused the G queries, key and value.
-std::size_t split_lds(const AttnShape& s, bool rope = false) {
+// LDS of the in-kernel merge (merge_chunks): one float4 and one (max, sum)
+// pair per thread.
+constexpr std::size_t kMergeLds = kThreads * (sizeof(floatx4) + sizeof(float2));
+
+// Slot merge buffers, plus with RoPE fused the G queries, key and value (and
+// at least the in-kernel merge's buffers when it merges its own chunks).
+std::size_t split_lds(const AttnShape& s, bool rope = false, bool merge_inside = false) {
     const std::size_t G = heads_per_block(s), hs = s.head_size;
     const std::size_t ns = kThreads / split_lanes(s);
-    return (G * ns * hs + 2 * G * ns + (rope ? (G + 2) * hs : 0)) * sizeof(float);
+    const std::size_t lds = (G * ns * hs + 2 * G * ns + (rope ? (G + 2) * hs : 0)) * sizeof(float);
+    return merge_inside && lds < kMergeLds ? kMergeLds : lds;
 }
 
 struct SplitScratch {
@@ -202,6 +208,10 @@ struct AttnArgs {
     const float* sin_t;
     float* kc_w;
     float* vc_w;
+    // Non-null: a row split over several chunks is merged by the last of
+    // its chunks' workgroups to finish (one counter per row and head group,
+    // zero between calls), not by a merge launch.
+    unsigned* merge_count;
 };
 
 // Lanes per key row: hs4 rounded up to a power of two, at most one wave.
@@ -214,6 +224,69 @@ __device__ __forceinline__ int lanes_per_row(int n) {
 // Positions a lane group loads per round, at most: all of a round's key and
 // value loads are issued before any is used.
 constexpr int kRoundPerSlot = 8;
+
+constexpr int kMergeDims = 8;
+constexpr int kSc1 = 16;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));  // the cache-policy operand's sc1 bit (device-coherent access)
+
+// The merge of the n chunks of heads h0 .. h0 + G - 1 of row i, inside the
+// split launch by the last of the row's chunk workgroups: the arithmetic of
+// attn_merge_kernel (below), which a merge launch would run, in the same
+// slots and order, so the result has its bits. Each (head, group of dpw
+// float4 columns) the merge kernel gives a workgroup is given a team of
+// used x dpw threads here, as many teams at once as 256 threads hold. The
+// chunks' partials, stored by other workgroups of this launch, are read with
+// device-coherent (sc1) loads.
+__device__ void merge_chunks(const AttnArgs& a, int i, int h0, int G, int n, float* lds) {
+    const int hs4 = a.head_size / 4;
+    const int dpw = hs4 < kMergeDims ? hs4 : kMergeDims, groups = (hs4 + dpw - 1) / dpw;
+    const int slots = kThreads / dpw, used = min(slots, (n + 7) / 8);
+    const int T = used * dpw, teams = kThreads / T, combos = G * groups;
+    floatx4* red4 = reinterpret_cast<floatx4*>(lds);
+    float2* red_ml = reinterpret_cast<float2*>(red4 + kThreads);
+    const __amdgpu_buffer_rsrc_t ors =
+        __builtin_amdgcn_make_buffer_rsrc(a.part_o, 0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t mrs =
+        __builtin_amdgcn_make_buffer_rsrc(a.part_ml, 0, 0x7fffffff, 0x00020000);
+    const int tid = threadIdx.x, team = tid / T, w = tid % T, r = w / dpw, dd = w % dpw;
+    for (int base = 0; base < combos; base += teams) {
+        const int combo = base + team;
+        const bool active = team < teams && combo < combos;
+        const int g = active ? combo / groups : 0;
+        const int d = (active ? combo % groups : 0) * dpw + dd;
+        const bool dok = d < hs4;
+        const int dl = dok ? d : hs4 - 1;  // past the head: computed, not stored
+        const uint32_t b = static_cast<uint32_t>((i * a.n_heads + h0 + g) * a.splits);
+        if (active) {
+            float m = -INFINITY, l = 0.0f;
+            floatx4 acc{0.f, 0.f, 0.f, 0.f};
+            for (int c0 = r; c0 < n; c0 += 8 * used) {
+                float2 ml[8];
+                floatx4 o[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const uint32_t c = b + min(c0 + u * used, n - 1);
+                    ml[u] = __builtin_bit_cast(
+                        float2, __builtin_amdgcn_raw_buffer_load_b64(mrs, c * 8, 0, kSc1));
+                    o[u] = __builtin_bit_cast(
+                        floatx4, __builtin_amdgcn_raw_buffer_load_b128(ors, (c * hs4 + dl) * 16, 0, kSc1));
+                }
+                merge_batch8(m, l, acc, ml, o, c0, used, n);
+            }
+            red4[team * T + r * dpw + dd] = acc;
+            if (dd == 0) red_ml[team * used + r] = make_float2(m, l);
+        }
+        __syncthreads();
+        if (active && w < dpw && dok) {
+            reinterpret_cast<floatx4*>(a.out + static_cast<std::size_t>(i) * a.out_stride +
+                                       static_cast<std::size_t>(h0 + g) * a.head_size)[d] =
+                merge_combine(used, floatx4{0.f, 0.f, 0.f, 0.f},
+                              [&](int rr) { return red_ml[team * used + rr]; },
+                              [&](int rr) { return red4[team * T + rr * dpw + w]; });
+        }
+        __syncthreads();
+    }
+}
 
 // Split workgroup: (head group hg, row i, chunk s). Thread = (slot, sub): the
 // LPP lanes of a slot share a position and hold float4 columns
@@ -447,11 +520,35 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
         if (nchunks == 1) {
             reinterpret_cast<floatx4*>(a.out + static_cast<std::size_t>(i) * a.out_stride +
                                        static_cast<std::size_t>(h0 + g) * hs)[d] = O * (1.0f / L);
+        } else if (a.merge_count) {
+            // Device-coherent stores: the row's last workgroup reads them.
+            const uint32_t c = static_cast<uint32_t>((head_row + g) * a.splits + s);
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(u32x4, O),
+                __builtin_amdgcn_make_buffer_rsrc(a.part_o, 0, 0x7fffffff, 0x00020000),
+                (c * hs4 + d) * 16, 0, kSc1);
+            if (d == 0)
+                __builtin_amdgcn_raw_buffer_store_b64(
+                    __builtin_bit_cast(u32x2, make_float2(M, L)),
+                    __builtin_amdgcn_make_buffer_rsrc(a.part_ml, 0, 0x7fffffff, 0x00020000),
+                    c * 8, 0, kSc1);
         } else {
             reinterpret_cast<floatx4*>(a.part_o)[((head_row + g) * a.splits + s) * hs4 + d] = O;
             if (d == 0) a.part_ml[(head_row + g) * a.splits + s] = make_float2(M, L);
         }
     }
+    if (nchunks == 1 || !a.merge_count) return;
+    // Counted in once every partial store above has landed; the last of the
+    // row's chunks merges them and sets the counter back to zero.
+    __shared__ unsigned arrived;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    unsigned* counter = a.merge_count + static_cast<std::size_t>(i) * gridDim.x + hg;
+    if (tid == 0) arrived = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (arrived != static_cast<unsigned>(nchunks - 1)) return;
+    merge_chunks(a, i, h0, G, nchunks, lds);
+    if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Merges the chunks of one (head, row): m = max m_c,
@@ -465,7 +562,6 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
 // the same on every call. (One workgroup per head took 8.7 us for 32 heads
 // x 256 chunks: four dependent batches in each of 32 workgroups; always
 // using every slot made 64 chunks slower, a 32-step combine.)
-constexpr int kMergeDims = 8;
 
 __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
     extern __shared__ floatx4 red4[];  // slots x dpw outputs, then slots x (max, sum)
@@ -837,7 +933,8 @@ template <int G, int LPP, int F, bool ROPE>
 void launch_split(const AttnShape& s, const AttnArgs& a, int rows, hipStream_t stream) {
     const dim3 grid(s.n_heads / G, rows, a.splits);
     hipLaunchKernelGGL((attn_split_kernel<G, LPP, F, ROPE>), grid, dim3(kThreads),
-                       split_lds(s, ROPE), stream, a);
+                       split_lds(s, ROPE, a.merge_count != nullptr), stream, a);
+    if (a.merge_count) return;  // the kernel merges its own rows
     if (a.splits < a.merge_from) return;  // e.g. one chunk per row: written directly
     launch_merge(s, a, rows, stream);
 }
@@ -982,8 +1079,10 @@ void run_attention(const AttnShape& s, int rows, const int* pos, const float* q,
 
 bool run_attention_rope(const AttnShape& s, const int* pos, const Summed& src, int dim,
                         int kv_dim, const float* cos_t, const float* sin_t, float* kc, float* vc,
-                        float* out, float* scratch, hipStream_t stream, SplitRow* defer) {
-    if (resolve(kAttnAutomatic, 1, s) != kAttnSplit || split_lds(s, true) > kMaxLds) return false;
+                        float* out, float* scratch, hipStream_t stream, SplitRow* defer,
+                        bool merge_inside) {
+    if (resolve(kAttnAutomatic, 1, s) != kAttnSplit || split_lds(s, true, true) > kMaxLds)
+        return false;
     if (src.n % 4 || src.mn % 4 || dim % 4 || kv_dim % 4) return false;
     if (!aligned16(src.slices == 1 ? src.c : src.partial) || (src.scale && !aligned16(src.scale)))
         return false;
@@ -1000,6 +1099,8 @@ bool run_attention_rope(const AttnShape& s, const int* pos, const Summed& src, i
     // longer ones (a shape with more splits) by the merge kernel, into out.
     const bool hold = defer && a.splits > 1;
     if (hold) a.merge_from = kMergeInGemv + 1;
+    if (!defer && merge_inside && a.splits > 1)
+        a.merge_count = tile_counters(static_cast<std::size_t>(s.n_heads / heads_per_block(s)));
     switch (heads_per_block(s)) {
         case 8: launch_split_g<8, true>(s, a, 1, stream); break;
         case 4: launch_split_g<4, true>(s, a, 1, stream); break;

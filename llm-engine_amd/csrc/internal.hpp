@@ -243,6 +243,9 @@ void run_attention(const AttnShape& s, int rows, const int* pos, const float* q,
 // k and v are written to the caches at *pos, and out receives attention over
 // positions 0 .. *pos. Scratch as run_attention's for one row. False
 // (nothing launched) for a shape or alignment it does not take.
+// With merge_inside (and no defer), a row split over several chunks is
+// merged inside the same launch by the last of its chunks to finish (the
+// merge kernel's arithmetic, so the same bits), not by a merge launch.
 // With defer, a row split over up to kMergeInGemv chunks is not merged:
 // *defer describes the chunks for the consumer to merge, run_skinny_merged
 // or run_attention_merge. `out` holds the row when it has one chunk, or
@@ -251,7 +254,7 @@ void run_attention(const AttnShape& s, int rows, const int* pos, const float* q,
 bool run_attention_rope(const AttnShape& s, const int* pos, const Summed& src, int dim,
                         int kv_dim, const float* cos_t, const float* sin_t, float* kc, float* vc,
                         float* out, float* scratch, hipStream_t stream,
-                        SplitRow* defer = nullptr);
+                        SplitRow* defer = nullptr, bool merge_inside = false);
 // The merge run_attention_rope left for its consumer, written to out.
 void run_attention_merge(const AttnShape& s, const SplitRow& r, float* out, hipStream_t stream);
 

@@ -288,7 +288,8 @@ private:
     // kernel that last wrote x for the next norm GEMV (dim % 64 == 0).
     bool use_ssq_ = false;
     // EM_DECODE_MERGE_KERNEL=1 at creation: one-row steps merge the
-    // attention chunks with the merge kernel, not in the wo GEMV (tests).
+    // attention chunks with the merge kernel, not in the wo GEMV (row-major
+    // path) or inside the split attention launch (strip path) (tests).
     bool merge_kernel_ = false;
     // EM_PREFILL_ROPE_FUSION=0 at creation: the exact-split qkv product of
     // prefill rows writes qkv_ and rope_cache_kernel follows, rather than
@@ -889,7 +890,8 @@ void Model::enqueue(int n) {
             const Summed qkv{qkv_.p, nullptr, nullptr, 1, qkv_cols,
                              static_cast<std::size_t>(qkv_cols)};
             if (!run_attention_rope(shape_, feed_dev_.p, qkv, D, KV, rope_cos_.p, rope_sin_.p,
-                                    L.kcache.p, L.vcache.p, att_.p, attn_scratch_.p, stream_)) {
+                                    L.kcache.p, L.vcache.p, att_.p, attn_scratch_.p, stream_,
+                                    nullptr, !merge_kernel_)) {
                 hipLaunchKernelGGL(rope_cache_kernel, dim3(ceil_div(rope_threads, kThreads), 1),
                                    dim3(kThreads), 0, stream_, qkv, qkv_cols, D, KV, hs,
                                    feed_dev_.p, rope_cos_.p, rope_sin_.p, qkv_.p, L.kcache.p,

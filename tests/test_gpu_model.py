@@ -394,3 +394,48 @@ def test_llama7b_shaped_model_matches_cpu(n_kv_heads):
     assert worst <= 1e-4 * max(1.0, scale) * 10, worst
     assert toks_g == toks_c
     gpu.close()
+
+
+@pytest.mark.parametrize("dim,hidden,heads,kv_heads",
+                         [(256, 688, 2, 2), (256, 688, 4, 2)], ids=["hs128_mha", "hs64_gqa"])
+def test_strip_decode_merges_chunks_inside_attention(tmp_path, monkeypatch, dim, hidden, heads,
+                                                     kv_heads):
+    # One-token steps over strip copies merge the split attention's chunks
+    # inside the attention launch: the last of a row's chunk workgroups to
+    # finish merges them, in the merge kernel's slots and order. A second
+    # model created with EM_DECODE_MERGE_KERNEL=1 launches the merge kernel
+    # instead, so every decode's logits must be the same bits; both against
+    # the CPU Transformer (greedy token equal, 1e-4 of the largest logit).
+    # Decodes from one chunk up to 16 and 32 chunks (hs128: 64-position
+    # chunks; hs64 with two heads per workgroup: 32-position chunks).
+    seq_len = 1024
+    m = e2e_model.fixture_model(heads, kv_heads, False, seed=dim + 11 * heads, dim=dim,
+                                hidden=hidden, vocab=320, seq_len=seq_len)
+    path = str(tmp_path / "model.bin")
+    e2e_model.write_raw(path, m)
+    ck = oracle.RefCheckpoint(lib, path)
+    w = ck.weights()
+    cpu = oracle.RefTransformer(lib, ck, True)
+    inside = em.Model(ck.config, w, q8=True)
+    monkeypatch.setenv("EM_DECODE_MERGE_KERNEL", "1")
+    launched = em.Model(ck.config, w, q8=True)
+    monkeypatch.delenv("EM_DECODE_MERGE_KERNEL")
+    V = ck.config["vocab_size"]
+    tokens = [(p * 11 + 5) % V for p in range(seq_len)]
+    pos = 0
+    for prefill_to, decode_to in ((40, 80), (500, 520), (990, 1024)):
+        part = tokens[pos:prefill_to]
+        a, b = inside.forward(part, pos), launched.forward(part, pos)
+        assert np.array_equal(a, b), f"prefill to {prefill_to}"
+        cpu.run(part, pos)
+        for pos in range(prefill_to, decode_to):
+            print(f"strip merge heads {heads}: decode {pos}", flush=True)
+            a, b = inside.forward(tokens[pos], pos), launched.forward(tokens[pos], pos)
+            assert np.array_equal(a, b), f"decode at {pos}: max diff {np.abs(a - b).max()}"
+            c = cpu.run([tokens[pos]], pos, True)
+            tol = 1e-4 * float(np.abs(c).max())
+            assert float(np.abs(a - c).max()) <= tol, f"decode at {pos}"
+            assert int(np.argmax(a)) == int(np.argmax(c)), f"greedy token at {pos}"
+        pos = decode_to
+    inside.close()
+    launched.close()
