@@ -1114,6 +1114,8 @@ bool run_attention_rope(const AttnShape& s, const int* pos, const Summed& src, i
     return true;
 }
 
+bool attention_merge_inside_preferred(const AttnShape& s) { return heads_per_block(s) == 1; }
+
 void run_attention_merge(const AttnShape& s, const SplitRow& r, float* out, hipStream_t stream) {
     AttnArgs a = base_args(s, 1, r.pos, nullptr, nullptr, nullptr, out);
     a.splits = r.splits;

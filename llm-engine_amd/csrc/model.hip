@@ -291,6 +291,11 @@ private:
     // attention chunks with the merge kernel, not in the wo GEMV (row-major
     // path) or inside the split attention launch (strip path) (tests).
     bool merge_kernel_ = false;
+    // Strip path: the split attention launch merges its own chunks where a
+    // workgroup serves one head (attention_merge_inside_preferred);
+    // EM_DECODE_MERGE_KERNEL=0 at creation makes it do so for every shape
+    // (tests).
+    bool merge_inside_ = false;
     // EM_PREFILL_ROPE_FUSION=0 at creation: the exact-split qkv product of
     // prefill rows writes qkv_ and rope_cache_kernel follows, rather than
     // RoPE and the cache write in the product's epilogue (tests).
@@ -373,6 +378,7 @@ void Model::init_runtime() {
     if (use_ssq_) ssq_.alloc(D / kSsqChunk);
     const char* mk = std::getenv("EM_DECODE_MERGE_KERNEL");
     merge_kernel_ = mk && std::atoi(mk) != 0;
+    merge_inside_ = mk ? !merge_kernel_ : attention_merge_inside_preferred(shape_);
     const char* rf = std::getenv("EM_PREFILL_ROPE_FUSION");
     rope_fusion_ = !rf || std::atoi(rf) != 0;
     const char* sf = std::getenv("EM_MODEL_SWIGLU_FUSION");
@@ -891,7 +897,7 @@ void Model::enqueue(int n) {
                              static_cast<std::size_t>(qkv_cols)};
             if (!run_attention_rope(shape_, feed_dev_.p, qkv, D, KV, rope_cos_.p, rope_sin_.p,
                                     L.kcache.p, L.vcache.p, att_.p, attn_scratch_.p, stream_,
-                                    nullptr, !merge_kernel_)) {
+                                    nullptr, merge_inside_)) {
                 hipLaunchKernelGGL(rope_cache_kernel, dim3(ceil_div(rope_threads, kThreads), 1),
                                    dim3(kThreads), 0, stream_, qkv, qkv_cols, D, KV, hs,
                                    feed_dev_.p, rope_cos_.p, rope_sin_.p, qkv_.p, L.kcache.p,

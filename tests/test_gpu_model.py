@@ -402,8 +402,10 @@ def test_strip_decode_merges_chunks_inside_attention(tmp_path, monkeypatch, dim,
                                                      kv_heads):
     # One-token steps over strip copies merge the split attention's chunks
     # inside the attention launch: the last of a row's chunk workgroups to
-    # finish merges them, in the merge kernel's slots and order. A second
-    # model created with EM_DECODE_MERGE_KERNEL=1 launches the merge kernel
+    # finish merges them, in the merge kernel's slots and order. The model
+    # created with EM_DECODE_MERGE_KERNEL=0 does so for every shape (by
+    # default only where a workgroup serves one head); a second model
+    # created with EM_DECODE_MERGE_KERNEL=1 launches the merge kernel
     # instead, so every decode's logits must be the same bits; both against
     # the CPU Transformer (greedy token equal, 1e-4 of the largest logit).
     # Decodes from one chunk up to 16 and 32 chunks (hs128: 64-position
@@ -416,6 +418,7 @@ def test_strip_decode_merges_chunks_inside_attention(tmp_path, monkeypatch, dim,
     ck = oracle.RefCheckpoint(lib, path)
     w = ck.weights()
     cpu = oracle.RefTransformer(lib, ck, True)
+    monkeypatch.setenv("EM_DECODE_MERGE_KERNEL", "0")
     inside = em.Model(ck.config, w, q8=True)
     monkeypatch.setenv("EM_DECODE_MERGE_KERNEL", "1")
     launched = em.Model(ck.config, w, q8=True)

@@ -1,7 +1,8 @@
 """GPU parity of 9 .. 16-row int8 products over the strip layout
 (strip_split.hip: one launch, its k slices added inside it), through
 em_matmul_q8_packed and through em_matmul_q8 over registered weights, against
-the CPU oracle.
+the CPU oracle; and of registered-weight batches of 9 .. 64 rows with every
+fusion and the ranged magnitudes.
 
 The reference runs these shapes as tiled_split plus sum_slices
 (cuda_matmul.cu:333-363, 245-254); its tests hold them to 1e-5 * k (2k with
@@ -101,7 +102,7 @@ def test_strip_4096_against_oracle(m, fusion):
         assert ratio.max() <= 1e-5, ratio.max()
 
 
-@pytest.mark.parametrize("fusion", ["plain", "rms_acc"])
+@pytest.mark.parametrize("fusion", ["plain", "acc", "rms", "rms_acc"])
 @pytest.mark.parametrize("m", [24, 32, 48, 64])
 def test_registered_batches_above_16_rows(m, fusion):
     # automatic over registered weights above 16 rows: the row-major exact
@@ -109,7 +110,8 @@ def test_registered_batches_above_16_rows(m, fusion):
     k = n = 4096
     A = inputs.normal((m, k), 1.0, 905 + m)
     q, s = orc.quantize_q8(inputs.normal((k, n), 0.02, 906))
-    acc = rms = fusion == "rms_acc"
+    acc = "acc" in fusion
+    rms = "rms" in fusion
     C0 = inputs.uniform((m, n), -1.0, 1.0, 907) if acc else None
     w = inputs.uniform((k,), 0.5, 1.5, 908) if rms else None
     outs = run_registered(A, q, s, C0, w)
@@ -218,6 +220,33 @@ def test_strip_tiny_magnitudes(shape):
     for norm in (False, True):
         outs = run_packed(A, q, s, w=w if norm else None)
         assert np.array_equal(outs[0], outs[1])
+        got = outs[0].astype(np.float64)
+        rows = fits if norm else np.ones(m, bool)
+        Ause = orc.rmsnorm(A[rows], w) if norm else A
+        err = np.abs(got[rows] - orc.matmul_f64(Ause, Bf))
+        bound = orc.abs_bound(Ause, Bf)
+        assert np.all(err <= 1e-4 * bound + floor), (norm, float((err / np.maximum(bound, 1e-300)).max()))
+        if norm:
+            assert np.all(got[~rows] == 0.0)
+
+
+@pytest.mark.parametrize("m", [9, 12, 16, 24, 32, 48, 64])
+def test_registered_ranged_magnitudes(m):
+    # The ranged rows through em_matmul_q8 over registered weights, at every
+    # batch size the decode batches use (the strip kernel up to 16 rows, the
+    # row-major exact split above): within 1e-4 * sum|a||w| of the f64
+    # product plus fp32's subnormal spacing, bit-identical on repeat, with
+    # and without the norm.
+    k = n = 4096
+    A = ranged_rows(m, k, 971 + m)
+    q, s = orc.quantize_q8(inputs.normal((k, n), 0.02, 972))
+    Bf = orc.dequantize(q, s)
+    w = inputs.uniform((k,), 0.5, 1.5, 973)
+    floor = 2.0 ** -149
+    fits = (A.astype(np.float64) ** 2).sum(axis=1) < float(np.finfo(np.float32).max)
+    for norm in (False, True):
+        outs = run_registered(A, q, s, w=w if norm else None)
+        assert np.array_equal(outs[0], outs[1]), "repeat not bit-identical"
         got = outs[0].astype(np.float64)
         rows = fits if norm else np.ones(m, bool)
         Ause = orc.rmsnorm(A[rows], w) if norm else A
