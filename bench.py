@@ -883,6 +883,88 @@ def floor_study(em, torch, reps: int = 20) -> dict:
     return out
 
 
+def floor_study_fp32(em, torch, reps: int = 20) -> dict:
+    """What bounds one fp32 m = 1 4096^2 call (BASELINE configs[0]'s shape on
+    the GPU), with the bench's method (HIP-graph replay of back-to-back
+    dependent launches over 10 rotating 64 MiB copies, 640 MiB):
+      empty     an empty 256-workgroup launch
+      read      em_probe_read of one copy per launch, contiguous chunks or a
+                grid stride, by workgroups and loads in flight
+      columns   em_probe_read_columns of one copy per launch: each workgroup
+                one seg-byte column run of every row of its k slice (the
+                layouts a GEMV over row-major weights can give its
+                workgroups), by segment, slices and XCD order
+      gemv      em_matmul_f32 (skinny): the split-K GEMV and its slice sum"""
+    out = {"method": "HIP-graph replay, HIP events on torch's stream; us per launch",
+           "matrix": "4096 x 4096 fp32 (64 MiB), 10 copies"}
+    copies, rows, row_bytes = 10, DIM, DIM * 4
+    nbytes = rows * row_bytes
+    g = graph_of(torch, lambda i: em.probe_empty(256), 2 * copies)
+    secs, _ = time_graph(torch, g, reps, 3)
+    out["empty_us"] = round(secs / (reps * 2 * copies) * 1e6, 3)
+    del g
+    bufs = [torch.ones((rows, DIM), dtype=torch.float32, device="cuda") for _ in range(copies)]
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+    def per_launch(fn):
+        graph = graph_of(torch, fn, copies)
+        secs, _ = time_graph(torch, graph, reps, 3)
+        del graph
+        us = secs / (reps * copies) * 1e6
+        return {"us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1)}
+
+    read = {}
+    for contig in (True, False):
+        for blocks in FLOOR_BLOCKS:
+            for depth in (8, 16):
+                read[f"{'contig' if contig else 'stride'} b{blocks} d{depth}"] = per_launch(
+                    lambda i, b=blocks, d=depth, c=contig: em.probe_read(bufs[i], sink, b, d, c))
+    out["read"] = read
+    best = min(read.items(), key=lambda kv: kv[1]["us"])
+    out["read_best"] = {"config": best[0], **best[1]}
+    progress("floor fp32: contiguous and strided reads done")
+    cols = {}
+    for seg in (64, 128, 256, 512, 1024):
+        groups = row_bytes // seg
+        for blocks in (256, 512, 1024):
+            slices = blocks // groups
+            if slices < 1:
+                continue
+            for depth in (8, 16):
+                for xcd in (False, True):
+                    cols[f"seg{seg} slices{slices} b{blocks} d{depth}{' xcd' if xcd else ''}"] = \
+                        per_launch(lambda i, sg=seg, sl=slices, d=depth, x=xcd:
+                                   em.probe_read_columns(bufs[i], rows, row_bytes, sg, sl, d, x, sink))
+    out["columns"] = cols
+    best = min(cols.items(), key=lambda kv: kv[1]["us"])
+    out["columns_best"] = {"config": best[0], **best[1]}
+    by_seg = {}
+    for key, v in cols.items():
+        seg = key.split()[0]
+        if seg not in by_seg or v["us"] < by_seg[seg]["us"]:
+            by_seg[seg] = {"config": key, **v}
+    out["columns_best_by_segment"] = by_seg
+    progress("floor fp32: column reads done")
+    del bufs
+    pool = Pool(em, torch, False, DIM, DIM, copies, 1000)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(8)
+    A = torch.randn((1, DIM), generator=gen, device="cuda", dtype=torch.float32)
+    C = torch.zeros((1, DIM), device="cuda")
+    graph = graph_of(torch, lambda i: em.matmul(A, pool.ws[i], C, kernel="skinny"), copies)
+    secs, _ = time_graph(torch, graph, reps, 3)
+    del graph
+    us = secs / (reps * copies) * 1e6
+    out["gemv"] = {"us": round(us, 3), "GBps": round(gemv_bytes(1, DIM, DIM, False) / us / 1e3, 1),
+                   "kernels": "gemv_kernel<float, 1, 4, 16> (64 k slices x 16 column tiles) + "
+                              "reduce_slices"}
+    pool.close()
+    del pool
+    torch.cuda.synchronize()
+    progress("floor fp32: GEMV done")
+    return out
+
+
 def single_launch_floor(em, torch, reps: int = 20) -> dict:
     """The headline call's floors, with its method (graph replay over 38
     rotating 16 MiB copies): an empty launch, and one launch reading a whole
@@ -973,6 +1055,8 @@ def main() -> int:
                     help="only time the Llama-7B-shaped forward pass L layers deep (32 for "
                          "the full model; builds ~0.8 GB of host weights per layer) and print "
                          "its JSON line")
+    ap.add_argument("--floor-fp32", action="store_true",
+                    help="the floor study of the fp32 m = 1 4096^2 call (JSON on stdout)")
     ap.add_argument("--floor", action="store_true",
                     help="only the floor study of the headline call (empty launches, "
                          "16 MiB and 600 MiB read sweeps, single-launch GEMV variants)")
@@ -1009,6 +1093,9 @@ def main() -> int:
         return 0
     if args.floor:
         print(json.dumps(floor_study(em, torch)))
+        return 0
+    if args.floor_fp32:
+        print(json.dumps(floor_study_fp32(em, torch)))
         return 0
     if args.profile_pass == "gemm":
         print(json.dumps(profile_gemm_pass(em, torch)))

@@ -189,6 +189,15 @@ int em_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream);
 int em_probe_empty(unsigned blocks, void* stream);
 int em_probe_read(const void* buf, size_t bytes, uint32_t* sink, unsigned blocks, unsigned depth,
                   int contiguous, void* stream);
+/* em_probe_read_columns reads a rows x row_bytes row-major matrix once (under
+ * 2^31 bytes, 16-byte aligned) the way a GEMV over row-major weights could
+ * split it: workgroup (g, s) reads bytes [g * seg_bytes, (g + 1) * seg_bytes)
+ * of every row of k slice s (slices of ceil(rows / slices) rows), seg_bytes
+ * 64, 128, 256, 512 or 1024, `depth` (8 or 16) 16-byte loads in flight per
+ * thread; with xcd != 0 (and a grid of a multiple of 8 workgroups) the
+ * workgroups one XCD runs own consecutive (g, s) pairs. */
+int em_probe_read_columns(const void* buf, unsigned rows, unsigned row_bytes, unsigned seg_bytes,
+                          unsigned slices, unsigned depth, int xcd, uint32_t* sink, void* stream);
 
 /* ---- Causal attention over a KV cache (cuda_attention.h) ------------------ */
 

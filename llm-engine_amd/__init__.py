@@ -29,7 +29,7 @@ EXPORTS = (
     "em_last_error", "em_available", "em_synchronize", "em_scratch_generation",
     "em_malloc", "em_free", "em_memcpy_h2d", "em_memcpy_d2h",
     "em_matmul_f32", "em_matmul_q8", "em_matmul_q8_noalloc", "em_quantize_q8", "em_dequantize_q8", "em_stream_read",
-    "em_probe_empty", "em_probe_read",
+    "em_probe_empty", "em_probe_read", "em_probe_read_columns",
     "em_pack_q8", "em_unpack_q8", "em_matmul_q8_packed",
     "em_q8_register", "em_q8_unregister", "em_q8_registered",
     "em_attention_check", "em_attention_scratch_floats", "em_attention",
@@ -134,6 +134,8 @@ def lib() -> ctypes.CDLL:
         L.em_q8_registered.argtypes = [_vp, _sz, _sz]
         L.em_probe_empty.argtypes = [ctypes.c_uint, _vp]
         L.em_probe_read.argtypes = [_vp, _sz, _vp, ctypes.c_uint, ctypes.c_uint, ctypes.c_int, _vp]
+        L.em_probe_read_columns.argtypes = [_vp, ctypes.c_uint, ctypes.c_uint, ctypes.c_uint,
+                                            ctypes.c_uint, ctypes.c_uint, ctypes.c_int, _vp, _vp]
         shp = ctypes.POINTER(AttentionShape)
         L.em_attention_check.argtypes = [shp, ctypes.c_int]
         L.em_attention_scratch_floats.argtypes = [shp, _sz, ctypes.c_int]
@@ -356,6 +358,13 @@ def registered_q8(q) -> bool:
 def probe_empty(blocks: int, stream=None) -> None:
     """em_probe_empty: one empty launch of `blocks` workgroups."""
     _check(lib().em_probe_empty(blocks, _stream_ptr(stream)))
+
+
+def probe_read_columns(buf, rows: int, row_bytes: int, seg_bytes: int, slices: int, depth: int,
+                       xcd: bool, sink, stream=None) -> None:
+    """em_probe_read_columns over a device tensor holding rows x row_bytes."""
+    _check(lib().em_probe_read_columns(buf.data_ptr(), rows, row_bytes, seg_bytes, slices, depth,
+                                       int(bool(xcd)), sink.data_ptr(), _stream_ptr(stream)))
 
 
 def probe_read(buf, sink, blocks: int, depth: int, contiguous: bool, stream=None) -> None:

@@ -652,6 +652,30 @@ int em_probe_read(const void* buf, size_t bytes, uint32_t* sink, unsigned blocks
     return EM_OK;
 }
 
+int em_probe_read_columns(const void* buf, unsigned rows, unsigned row_bytes, unsigned seg_bytes,
+                          unsigned slices, unsigned depth, int xcd, uint32_t* sink, void* stream) {
+    if (rows == 0) return EM_OK;
+    if (!buf || !sink) return fail(EM_EINVAL, "probe_read_columns: null pointer");
+    if (seg_bytes < 64 || seg_bytes > 1024 || (seg_bytes & (seg_bytes - 1)))
+        return fail(EM_EINVAL, "probe_read_columns: segment must be 64, 128, 256, 512 or 1024 bytes");
+    if (row_bytes == 0 || row_bytes % seg_bytes || reinterpret_cast<uintptr_t>(buf) % 16)
+        return fail(EM_EINVAL, "probe_read_columns: rows must be whole segments, buffer 16-byte aligned");
+    if (static_cast<unsigned long long>(rows) * row_bytes >= (1ULL << 31))
+        return fail(EM_EINVAL, "probe_read_columns: at most 2^31 bytes");
+    if (slices == 0 || slices > rows) return fail(EM_EINVAL, "probe_read_columns: 1..rows slices");
+    if (static_cast<unsigned long long>(row_bytes / seg_bytes) * slices > 65535)
+        return fail(EM_EINVAL, "probe_read_columns: at most 65535 workgroups");
+    if (depth != 8 && depth != 16) return fail(EM_EINVAL, "probe_read_columns: depth must be 8 or 16");
+    if (!em::device_present()) return fail(EM_ENODEV, "probe_read_columns: no usable GPU");
+    em::run_probe_read_columns(buf, static_cast<int>(rows), static_cast<int>(row_bytes),
+                               static_cast<int>(seg_bytes), static_cast<int>(slices),
+                               static_cast<int>(depth), xcd != 0, sink,
+                               static_cast<hipStream_t>(stream));
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail(EM_EDEVICE, std::string("hip: launch: ") + hipGetErrorString(err));
+    return EM_OK;
+}
+
 static em::AttnShape to_shape(const em_attention_shape& s) {
     return {s.n_heads, s.n_kv_heads, s.head_size, s.seq_len, s.q_stride, s.kv_stride, s.out_stride};
 }

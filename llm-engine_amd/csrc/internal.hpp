@@ -178,6 +178,13 @@ void run_stream_read(const void* buf, std::size_t bytes, uint32_t* sink, hipStre
 void run_probe_empty(int blocks, hipStream_t stream);
 bool run_probe_read(const void* buf, std::size_t bytes, int blocks, int depth, bool contig,
                     uint32_t* sink, hipStream_t stream);
+// One read of a rows x row_bytes matrix, workgroup (group, slice) taking the
+// seg_bytes-wide column run `group` (64 .. 1024, a power of two dividing
+// row_bytes) of rows [slice * span, ...), span = ceil(rows / slices); depth
+// 8 or 16 (false for another seg_bytes or depth). xcd: each XCD's
+// workgroups own consecutive (group, slice) pairs.
+bool run_probe_read_columns(const void* buf, int rows, int row_bytes, int seg_bytes, int slices,
+                            int depth, bool xcd, uint32_t* sink, hipStream_t stream);
 
 // The strip layout of int8 weights (gemv_packed.hip): n / 16 strips of 16
 // columns, strip j holding rows 0 .. k - 1 of columns 16j .. 16j + 15

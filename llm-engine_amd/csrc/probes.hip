@@ -1,6 +1,7 @@
 // Measurement kernels for the floor study in bench.py (--floor): what one
 // dependent launch costs with no work, and how fast one launch can read a
-// buffer, by grid size, loads in flight and access pattern. No counterpart in
+// buffer, by grid size, loads in flight and access pattern (contiguous
+// chunks, a grid stride, or the column segments of a row-major matrix). No counterpart in
 // the reference; the reference's bench times a device-to-device copy as its
 // ceiling (bench_cuda.cpp:79-88).
 #include <algorithm>
@@ -60,7 +61,71 @@ void launch_read(const void* buf, std::size_t n16, int blocks, bool contig, uint
     }
 }
 
+// A rows x row_bytes matrix read by column segments: workgroup b owns the
+// SEG-byte run [group * SEG, (group + 1) * SEG) of every row of its k slice
+// (rows [slice * span, (slice + 1) * span)), 256 threads as SEG / 16 lanes
+// across the run and 256 / (SEG / 16) rows per load round, DEPTH rounds in
+// flight per thread; with xcd, the workgroups of one XCD own consecutive
+// (group, slice) pairs, a band of columns. The layouts a GEMV over row-major
+// weights can give its workgroups, read with nothing else done. Rows past
+// the slice are clamped to its last (read again, never out of bounds).
+template <int SEG, int DEPTH>
+__global__ __launch_bounds__(kThreads) void read_columns_kernel(const char* p, int rows,
+                                                                int row_bytes, int span,
+                                                                int slices, int xcd,
+                                                                uint32_t* sink) {
+    constexpr int kLanes = SEG / 16;
+    constexpr int kRound = kThreads / kLanes;
+    const int total = gridDim.x;
+    const int id = xcd ? (blockIdx.x & 7) * (total / 8) + (blockIdx.x >> 3) : blockIdx.x;
+    const int group = id / slices, slice = id - group * slices;
+    const int rb = slice * span, re = min(rb + span, rows);
+    const size_t col = static_cast<size_t>(group) * SEG + 16 * (threadIdx.x % kLanes);
+    uint32_t acc = 0;
+    for (int r = rb + threadIdx.x / kLanes; r < re; r += kRound * DEPTH) {
+        uint4 v[DEPTH];
+#pragma unroll
+        for (int u = 0; u < DEPTH; ++u) {
+            const int rr = min(r + u * kRound, re - 1);
+            v[u] = stream_load(reinterpret_cast<const uint4*>(p + static_cast<size_t>(rr) * row_bytes + col));
+        }
+#pragma unroll
+        for (int u = 0; u < DEPTH; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    if (acc == 0x9e3779b9u) *sink = acc;
+}
+
+template <int SEG>
+void launch_columns(const void* buf, int rows, int row_bytes, int span, int slices, int blocks,
+                    int xcd, int depth, uint32_t* sink, hipStream_t s) {
+    const char* p = static_cast<const char*>(buf);
+    if (depth == 8) {
+        hipLaunchKernelGGL((read_columns_kernel<SEG, 8>), dim3(blocks), dim3(kThreads), 0, s, p,
+                           rows, row_bytes, span, slices, xcd, sink);
+    } else {
+        hipLaunchKernelGGL((read_columns_kernel<SEG, 16>), dim3(blocks), dim3(kThreads), 0, s, p,
+                           rows, row_bytes, span, slices, xcd, sink);
+    }
+}
+
 }  // namespace
+
+bool run_probe_read_columns(const void* buf, int rows, int row_bytes, int seg_bytes, int slices,
+                            int depth, bool xcd, uint32_t* sink, hipStream_t stream) {
+    if (depth != 8 && depth != 16) return false;
+    const int groups = row_bytes / seg_bytes;
+    const int blocks = groups * slices;
+    const int span = (rows + slices - 1) / slices;
+    const int x = xcd && blocks % 8 == 0 ? 1 : 0;
+    switch (seg_bytes) {
+        case 64: launch_columns<64>(buf, rows, row_bytes, span, slices, blocks, x, depth, sink, stream); return true;
+        case 128: launch_columns<128>(buf, rows, row_bytes, span, slices, blocks, x, depth, sink, stream); return true;
+        case 256: launch_columns<256>(buf, rows, row_bytes, span, slices, blocks, x, depth, sink, stream); return true;
+        case 512: launch_columns<512>(buf, rows, row_bytes, span, slices, blocks, x, depth, sink, stream); return true;
+        case 1024: launch_columns<1024>(buf, rows, row_bytes, span, slices, blocks, x, depth, sink, stream); return true;
+        default: return false;
+    }
+}
 
 void run_probe_empty(int blocks, hipStream_t stream) {
     hipLaunchKernelGGL(empty_kernel, dim3(blocks), dim3(kThreads), 0, stream);

@@ -207,6 +207,15 @@ def test_probes_check_before_the_gpu():
     assert L.em_probe_read(16, 64, 16, 256, 5, 0, None) == em.EM_EINVAL
     assert b"depth" in L.em_last_error()
     assert L.em_probe_read(16, 64, 16, 0, 8, 0, None) == em.EM_EINVAL
+    # rows, row_bytes, seg_bytes, slices, depth, xcd
+    assert L.em_probe_read_columns(16, 4, 1024, 96, 1, 8, 0, 16, None) == em.EM_EINVAL
+    assert b"segment" in L.em_last_error()
+    assert L.em_probe_read_columns(16, 4, 1000, 64, 1, 8, 0, 16, None) == em.EM_EINVAL
+    assert L.em_probe_read_columns(16, 4, 1024, 64, 5, 8, 0, 16, None) == em.EM_EINVAL
+    assert L.em_probe_read_columns(16, 4, 1024, 64, 1, 4, 0, 16, None) == em.EM_EINVAL
+    assert b"depth" in L.em_last_error()
+    assert L.em_probe_read_columns(16, 1 << 20, 4096, 64, 1, 8, 0, 16, None) == em.EM_EINVAL
+    assert L.em_probe_read_columns(16, 0, 1024, 64, 1, 8, 0, 16, None) == em.EM_OK
 
 
 def test_q8_register_checks_before_the_gpu():
