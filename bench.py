@@ -610,21 +610,22 @@ def profile_pass(em, torch, sweeps: int = 2) -> dict:
 
 
 def profile_smallm_pass(em, torch, reps: int = 20) -> dict:
-    """Eager int8 products at m = 4, 8, 16 and 64 over the rotating 4096^2
-    pool of registered weights, as bench.py's decode rows (automatic: the
-    strip-copy MFMA kernel at 4 and 8 rows, the exact-split kernel at 16 and
-    64), for counter passes over the decode-batch kernels."""
+    """Eager int8 products at m = 4, 8, 16, 32 and 64 over the rotating
+    4096^2 pool of registered weights, as bench.py's decode rows (automatic:
+    the strip-copy MFMA kernel at 4 and 8 rows, the strip-copy exact split
+    at 16, the row-major exact split and its slice sum at 32 and 64), for
+    counter passes over the decode-batch kernels."""
     per_copy = DIM * DIM
     copies = -(-POOL_MIN_BYTES // per_copy)
     pool = Pool(em, torch, True, DIM, DIM, copies, 1000, register=True)
-    for m in (4, 8, 16, 64):
+    for m in (4, 8, 16, 32, 64):
         A = torch.randn((m, DIM), device="cuda")
         C = torch.empty((m, DIM), device="cuda")
         for i in range(reps):
             em.matmul(A, pool.ws[i % copies], C, scale=pool.scales[i % copies])
         torch.cuda.synchronize()
     pool.close()
-    return {"m": [4, 8, 16, 64], "launches_each": reps}
+    return {"m": [4, 8, 16, 32, 64], "launches_each": reps}
 
 
 def profile_gemm_pass(em, torch, reps: int = 5, warm_s: float = 0.3) -> dict:

@@ -185,8 +185,9 @@ def test_decode_merge_inside_wo_gemv(tmp_path, monkeypatch, dim, hidden, heads, 
 
 
 @pytest.mark.parametrize("dim,hidden,heads,kv_heads",
-                         [(256, 688, 4, 2), (320, 864, 5, 5), (192, 512, 6, 2)],
-                         ids=["d256_gqa", "d320_mha", "d192_group3"])
+                         [(256, 688, 4, 2), (320, 864, 5, 5), (192, 512, 6, 2),
+                          (256, 4608, 4, 2)],
+                         ids=["d256_gqa", "d320_mha", "d192_group3", "d256_wide_ffn"])
 def test_strip_copy_decode_matches_cpu(tmp_path, monkeypatch, dim, hidden, heads, kv_heads):
     # int8 with a vocabulary of 320 (a multiple of 16): every projection
     # takes a strip-layout copy, so one-token steps run each product as one
@@ -197,7 +198,9 @@ def test_strip_copy_decode_matches_cpu(tmp_path, monkeypatch, dim, hidden, heads
     # w13 product, which must give the fused model's logits bit for bit.
     # Every decode over the context, then a chunked and a whole prefill
     # (row-major either way), each model against the CPU Transformer within
-    # the 3e-5 of the largest logit used above, greedy token equal.
+    # the 3e-5 of the largest logit used above, greedy token equal. With
+    # hidden 4608 the w13 product has 576 strips (288 gate | up pairs), more
+    # workgroups than the 256 CUs in both w13 paths.
     m = e2e_model.fixture_model(heads, kv_heads, False, seed=dim + 3 * heads, dim=dim,
                                 hidden=hidden, vocab=320, seq_len=24)
     path = str(tmp_path / "model.bin")

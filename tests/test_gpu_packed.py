@@ -165,7 +165,7 @@ def test_packed_graph_replay_matches_eager():
 # ---- registered weights: em_matmul_q8 over the strip copy -------------------
 
 REG_SHAPES = [(288, 864), (4096, 4096), (8192, 64), (11008, 64), (11008, 4096), (768, 288),
-              (288, 32000), (20, 48)]
+              (288, 32000), (20, 48), (4096, 12288), (3000, 8192), (4096, 32000)]
 
 
 @pytest.mark.parametrize("fusion", ["plain", "rms"])
@@ -461,3 +461,49 @@ def test_registered_misaligned_norm_weight(shape, m):
         em.unregister_q8(qd)
     want = orc.matmul_fused(A, Bq=q, scale=s, w=w)
     check(got, want, orc.rmsnorm(A, w), orc.dequantize(q, s), k, 2.0)
+
+
+@pytest.mark.parametrize("fusion", ["plain", "acc", "rms", "rms_acc"])
+@pytest.mark.parametrize("shape", [(4096, 12288), (3000, 8192), (288, 32000), (4096, 4112),
+                                   (1024, 16384)], ids=lambda s: "x".join(map(str, s)))
+def test_registered_wide_rows_match_narrow_bit_for_bit(shape, fusion):
+    # Past one strip per CU the strip kernel's grid runs in rounds; a
+    # strip's sums do not depend on its round or on the other strips. So
+    # columns [c0, c0 + 4096) of the wide product equal, bit for bit, the
+    # product of those 4096 columns registered on their own (256 strips, one
+    # round): checked at the first, a middle and the last block of columns,
+    # and against the oracle.
+    k, n = shape
+    A = inputs.uniform((1, k), -1.0, 1.0, 61)
+    q, s = orc.quantize_q8(inputs.normal((k, n), 0.02, 62))
+    acc = "acc" in fusion
+    rms = "rms" in fusion
+    C0 = inputs.uniform((1, n), -1.0, 1.0, 63) if acc else None
+    w = inputs.uniform((k,), 0.5, 1.5, 64) if rms else None
+    dA, wd = dev(A), (dev(w) if rms else None)
+    qd, sd = dev(q), dev(s)
+    em.register_q8(qd)
+    try:
+        C = dev(C0) if acc else torch.empty((1, n), device="cuda")
+        em.matmul(dA, qd, C, scale=sd, accumulate=acc, rms_weight=wd)
+        wide = host(C)
+        C2 = dev(C0) if acc else torch.empty((1, n), device="cuda")
+        em.matmul(dA, qd, C2, scale=sd, accumulate=acc, rms_weight=wd)
+        assert np.array_equal(wide, host(C2)), "repeat not bit-identical"
+    finally:
+        em.unregister_q8(qd)
+    for c0 in sorted({0, (n // 2 - 2048) // 16 * 16, n - 4096}):
+        qn = dev(np.ascontiguousarray(q[:, c0:c0 + 4096]))
+        sn = dev(np.ascontiguousarray(s[c0:c0 + 4096]))
+        em.register_q8(qn)
+        try:
+            Cn = dev(np.ascontiguousarray(C0[:, c0:c0 + 4096])) if acc else \
+                torch.empty((1, 4096), device="cuda")
+            em.matmul(dA, qn, Cn, scale=sn, accumulate=acc, rms_weight=wd)
+            narrow = host(Cn)
+        finally:
+            em.unregister_q8(qn)
+        assert np.array_equal(wide[:, c0:c0 + 4096], narrow), f"columns from {c0}"
+    want = orc.matmul_fused(A, Bq=q, scale=s, w=w, C0=C0)
+    An = orc.rmsnorm(A, w) if rms else A
+    check(wide, want, An, orc.dequantize(q, s), k, 2.0 if (acc or rms) else 1.0, C0)
