@@ -703,7 +703,18 @@ bool run_split_bf16(const MatmulArgs& a, const RopeFuse* rope) {
         const double rounds = grid / cu_count();
         return rounds <= 1.0 || rounds / std::ceil(rounds) >= (raw ? 0.8 : 0.7);
     };
-    const int RB = fits(4) ? 4 : fits(2) ? 2 : 1;
+    // A four-block grid that must still split k (fewer tiles than CUs)
+    // loses to the two-block grid of twice the tiles that need not: no
+    // partials and no slice-sum launch, for a second widening of each
+    // weight. Same box, µs (two-block / four-block with its k split, best of
+    // three): 11008 x 4096 at m = 512 126.7 / 134.5, m = 768 197.5 / 202.6;
+    // 8192 x 4096 at m = 512 87.7 / 104.8; 5120 x 4096 at m = 512 71.7 /
+    // 73.3; 11008 x 2048 at m = 1024 123.8 / 131.6.
+    auto tiles = [&](int rb) {
+        return static_cast<long long>(ceil_div(a.m, 16 * rb)) * col_tiles;
+    };
+    int RB = fits(4) ? 4 : fits(2) ? 2 : 1;
+    if (RB == 4 && tiles(4) < cu_count() && tiles(2) >= cu_count() && fits(2)) RB = 2;
     const int row_tiles = ceil_div(a.m, 16 * RB);
     const int m_pad = row_tiles * 16 * RB;
     const int k_pad = ceil_div(a.k, kChunk) * kChunk;
