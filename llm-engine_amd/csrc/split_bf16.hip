@@ -703,20 +703,10 @@ bool run_split_bf16(const MatmulArgs& a, const RopeFuse* rope) {
         const double rounds = grid / cu_count();
         return rounds <= 1.0 || rounds / std::ceil(rounds) >= (raw ? 0.8 : 0.7);
     };
-    // A four-block grid that must still split k (at most half a tile per
-    // CU) loses to the two-block grid of twice the tiles that need not: no
-    // partials and no slice-sum launch, for a second widening of each
-    // weight. Same box, µs (two-block / four-block with its k split, best of
-    // three), weights resident in the Infinity Cache: 11008 x 4096 at m = 512
-    // 126.7 / 134.5, m = 768 197.5 / 202.6; 8192 x 4096 at m = 512 87.7 /
-    // 104.8; 11008 x 2048 at m = 1024 123.8 / 131.6. With the weights
-    // rotated through HBM: 8192 x 4096 87.5 / 97.1, 11008 x 4096 even
-    // (131.7 / 133.9).
     auto tiles = [&](int rb) {
         return static_cast<long long>(ceil_div(a.m, 16 * rb)) * col_tiles;
     };
     int RB = fits(4) ? 4 : fits(2) ? 2 : 1;
-    if (RB == 4 && 2 * tiles(4) <= cu_count() && tiles(2) >= cu_count() && fits(2)) RB = 2;
     // Four-block tiles whose last round is at most half full also win when
     // that round runs as two-block tiles (the tail below), though the rounds
     // rule above turns them down: 4096 x 11008 at m = 512 131.9 against
