@@ -148,6 +148,13 @@ struct RopeFuse {
 // q is stored rotated, k rotated into kc and v into vc (not into C), with
 // rope_cache_kernel's arithmetic; returns true. Otherwise C as usual, false.
 bool run_split_bf16(const MatmulArgs& a, const RopeFuse* rope = nullptr);
+// The forward pass's w13 with its SwiGLU: B (k x 2 hidden) holds gates then
+// ups, a.C is hidden wide and gets silu(gate) * up, the bits of the product
+// followed by swiglu_kernel. False, nothing launched, when the shape is not
+// supported (hidden % 16, alignment, accumulate) or the product would need
+// a k split.
+bool split_bf16_swiglu_supported(const MatmulArgs& a, int hidden);
+bool run_split_bf16_swiglu(const MatmulArgs& a, int hidden);
 // True if automatic sends an int8 product of m rows (k x n weights) to the
 // exact-split kernel rather than the GEMV.
 bool split_bf16_preferred(int m, int n, int k);

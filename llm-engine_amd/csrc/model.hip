@@ -264,6 +264,7 @@ private:
                           const float* ssq);
     bool residual(int n, const float* in, const Proj& w);
     bool residual_merged(const SplitRow& att, const Proj& w);
+    bool swiglu_pair(int n, const LayerDev& L);
     bool qkv_exact_split(int n, LayerDev& L, bool* roped);
     bool swiglu_w2(const Summed& gu, const Proj& w2, bool* wrote_ssq);
     void reserve_rows(std::size_t n);
@@ -306,9 +307,10 @@ private:
     // merging its own chunks and swiglu_kernel between w13 and w2.
     // EM_MODEL_STRIPS=0 at creation keeps the row-major decode path.
     bool strips_ = false;
-    // Over the strips, w13 and the SwiGLU are one launch (run_gemv_swiglu:
-    // the same bits); EM_MODEL_SWIGLU_FUSION=0 at creation runs
-    // swiglu_kernel after the w13 product instead (tests).
+    // Over the strips, w13 and the SwiGLU are one launch (run_gemv_swiglu),
+    // and so are they for int8 rows past 16 (swiglu_pair): the same bits;
+    // EM_MODEL_SWIGLU_FUSION=0 at creation runs swiglu_kernel after the w13
+    // product instead (tests).
     bool swiglu_fusion_ = true;
     void register_strips();
     Buf<float> ssq_;
@@ -858,6 +860,21 @@ bool Model::swiglu_w2(const Summed& gu, const Proj& w2, bool* wrote_ssq) {
     return slices > 0;
 }
 
+// Rows past 16 of an int8 model: hb = silu(gate) * up straight from the
+// exact-split w13 product (run_split_bf16_swiglu), which the product
+// followed by swiglu_kernel gives bit for bit, with half the product's
+// stores and one launch fewer. (Up to 16 rows `automatic` may run the
+// strip-copy kernels instead, so those rows keep the two launches.) False,
+// nothing launched, where it does not take the shape.
+bool Model::swiglu_pair(int n, const LayerDev& L) {
+    if (!q8_ || !swiglu_fusion_ || n <= 16) return false;
+    const MatmulArgs a = gemv_args(n, x_.p, L.w13, hb_.p, L.rms_ffn.p, false, nullptr);
+    if (!split_bf16_preferred(a.m, a.n, a.k) || !run_split_bf16_swiglu(a, cfg_.hidden_dim))
+        return false;
+    check(hipGetLastError(), "launch");
+    return true;
+}
+
 void Model::reserve_rows(std::size_t n) {
     if (n <= rows_) return;
     check(hipStreamSynchronize(stream_), "synchronize before growth");
@@ -943,6 +960,11 @@ void Model::enqueue(int n) {
                           attn_scratch_.p, kAttnAutomatic, stream_);
         }
         have_ssq = chunks.o ? residual_merged(chunks, L.wo) : residual(n, att_.p, L.wo);
+        if (swiglu_pair(n, L)) {
+            project(n, hb_.p, L.w2, x_.p, nullptr, true);
+            have_ssq = false;
+            continue;
+        }
         const Summed gu = project_summed(n, x_.p, L.w13, gu_.p, L.rms_ffn.p,
                                          have_ssq ? ssq_.p : nullptr);
         if (!(n == 1 && swiglu_w2(gu, L.w2, &have_ssq))) {

@@ -278,6 +278,10 @@ struct SbParams {
     int accumulate, direct;
     int row_tiles, col_tiles, xcd_order;
     int col_base;  // first column tile of this launch
+    // PAIR kernels (the forward pass's w13 with its SwiGLU): B's first
+    // `pair` columns are gates and the next `pair` ups; a column tile holds
+    // 128 gates and their 128 ups, and out (m x pair) gets silu(g) * u.
+    int pair;
     RopeFuse rope;  // direct only: rope.pos non-null fuses RoPE and the cache write
 };
 
@@ -421,8 +425,14 @@ __device__ __forceinline__ bf16x8 column(const uint4 (&b)[8], int t) {
 // RAW: A arrives as fp32 and is split in registers (else as the three planes
 // of split_a_kernel). WHOLE: k is a multiple of the chunk, so every chunk
 // lies inside k and no row or value needs a clamp or a mask.
-template <int RB, bool RAW, bool WHOLE>
+// PAIR (pre-split planes only, one slice): lanes j < 8 load gate columns
+// c0 + 16j .., lanes j >= 8 the up columns of the same gates, so tile
+// column t < 128 is gate c0 + t and column 128 + t its up; the epilogue
+// writes silu(g) * u of the finished, scaled values: the bits of the
+// product written to C followed by the forward pass's SwiGLU kernel.
+template <int RB, bool RAW, bool WHOLE, bool PAIR = false>
 __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
+    static_assert(!(PAIR && RAW), "the SwiGLU pair reads pre-split planes");
     __shared__ __attribute__((aligned(16))) floatx4 tile[4 * 16 * kTile / 4];
 
     const int tid = threadIdx.x;
@@ -431,7 +441,7 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
     const int g = lane >> 4, j = lane & 15;
     const TileId place = tile_of(blockIdx.x, gridDim.x, p.row_tiles, p.col_tiles,
                                  p.xcd_order != 0);
-    const int c0 = (place.col + p.col_base) * kTile;
+    const int c0 = (place.col + p.col_base) * (PAIR ? kTile / 2 : kTile);
     const int m0 = place.row * 16 * RB;
     const int kb = place.slice * p.k_span;
     const int ke = min(p.k, kb + p.k_span);
@@ -445,7 +455,11 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
     // A lane whose columns lie past n reads column 0 (its sums are never
     // stored); rows past k read row k - 1, whose A3 entries are zero. No
     // load is predicated, so each multiply waits only for its own chunk.
-    const int col = c0 + 16 * j < p.n ? c0 + 16 * j : 0;
+    int col = c0 + 16 * j < p.n ? c0 + 16 * j : 0;
+    if constexpr (PAIR) {
+        const int gate = c0 + 16 * (j & 7);
+        col = gate < p.pair ? (j < 8 ? gate : p.pair + gate) : 0;
+    }
     const std::size_t plane = static_cast<std::size_t>(p.m_pad) * p.k_pad;
     // This lane's rows of A (rows past m read row m - 1; their sums are
     // never stored), from which each chunk is one offset away.
@@ -574,6 +588,41 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
                     floatx4{acc[rb][4 * q][r], acc[rb][4 * q + 1][r], acc[rb][4 * q + 2][r],
                             acc[rb][4 * q + 3][r]};
         __syncthreads();
+        if constexpr (PAIR) {
+            // Eight gates of one row per thread and their ups 128 columns
+            // on, each summed over the waves in order as below, scaled as C
+            // would be written, then paired.
+            const int prow = tid / 16, pp = (tid % 16) * 8;
+            const int prow_m = m0 + 16 * rb + prow;
+            floatx4 gv[2], uv[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int gq = granule(pp / 4 + q), uq = granule((pp + kTile / 2) / 4 + q);
+                gv[q] = tile[prow * (kTile / 4) + gq];
+                uv[q] = tile[prow * (kTile / 4) + uq];
+#pragma unroll
+                for (int ww = 1; ww < 4; ++ww) {
+                    gv[q] += tile[(ww * 16 + prow) * (kTile / 4) + gq];
+                    uv[q] += tile[(ww * 16 + prow) * (kTile / 4) + uq];
+                }
+            }
+            if (prow_m < p.m) {
+                const int sh = -p.shifts[prow_m];
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const int c = c0 + pp + 4 * q;
+                    if (c >= p.pair) break;
+                    floatx4 gx = gv[q] * *reinterpret_cast<const floatx4*>(p.scale + c);
+                    floatx4 ux = uv[q] * *reinterpret_cast<const floatx4*>(p.scale + p.pair + c);
+                    floatx4 y;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        y[e] = silu_mul(__builtin_ldexpf(gx[e], sh), __builtin_ldexpf(ux[e], sh));
+                    *reinterpret_cast<floatx4*>(p.out + static_cast<std::size_t>(prow_m) * p.pair + c) = y;
+                }
+            }
+            continue;
+        }
         const int row = m0 + 16 * rb + orow;
         floatx4 v[4];
 #pragma unroll
@@ -642,6 +691,13 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
 template <int RB>
 void launch(const SbParams& p, int blocks, bool raw, hipStream_t s) {
     const bool whole = p.k % kChunk == 0;
+    if (p.pair) {
+        if (whole)
+            hipLaunchKernelGGL((split_bf16_kernel<RB, false, true, true>), dim3(blocks), dim3(kThreads), 0, s, p);
+        else
+            hipLaunchKernelGGL((split_bf16_kernel<RB, false, false, true>), dim3(blocks), dim3(kThreads), 0, s, p);
+        return;
+    }
     if (raw && whole) {
         hipLaunchKernelGGL((split_bf16_kernel<RB, true, true>), dim3(blocks), dim3(kThreads), 0, s, p);
     } else if (raw) {
@@ -675,11 +731,17 @@ bool split_bf16_preferred(int m, int n, int k) {
     return m >= 5 || (m >= 3 && w >= (1LL << 25)) || (m >= 2 && w >= (1LL << 26));
 }
 
-bool run_split_bf16(const MatmulArgs& a, const RopeFuse* rope) {
+namespace {
+
+// The product, or with pair > 0 the SwiGLU pair (out = a.C, m x pair);
+// false when pair is asked for and the product would need a k split (then
+// nothing is launched). *fused: RoPE was fused.
+bool split_run(const MatmulArgs& a, const RopeFuse* rope, int pair, bool* fused) {
     // Without a norm, the kernel splits A itself, chunk by chunk (needs whole
     // 8-value groups and 16-byte rows); otherwise a pre-pass writes the three
-    // planes with the norm fused.
-    const bool raw = !a.rms_weight && a.k % 8 == 0 && reinterpret_cast<uintptr_t>(a.A) % 16 == 0;
+    // planes with the norm fused. The SwiGLU pair always reads the planes.
+    const bool raw = !pair && !a.rms_weight && a.k % 8 == 0 &&
+                     reinterpret_cast<uintptr_t>(a.A) % 16 == 0;
 
     // More 16-row blocks per workgroup cut how often each weight is widened
     // (the VALU work that paces this kernel); fewer keep more workgroups in
@@ -720,6 +782,15 @@ bool run_split_bf16(const MatmulArgs& a, const RopeFuse* rope) {
     const int m_pad = row_tiles * 16 * RB;
     const int k_pad = ceil_div(a.k, kChunk) * kChunk;
 
+    // k slices up to one workgroup per CU, each at least 256 rows deep.
+    const long long blocks = static_cast<long long>(row_tiles) * col_tiles;
+    const int want = static_cast<int>(std::max(1LL, cu_count() / blocks));
+    int slices = std::max(1, std::min(want, ceil_div(a.k, 256)));
+    const int span = ceil_div(ceil_div(a.k, slices), kStep) * kStep;
+    slices = ceil_div(a.k, span);
+
+    if (pair && slices > 1) return false;
+
     uint16_t* A3 = nullptr;
     int* shifts = nullptr;
     if (!raw) {
@@ -746,13 +817,6 @@ bool run_split_bf16(const MatmulArgs& a, const RopeFuse* rope) {
         }
     }
 
-    // k slices up to one workgroup per CU, each at least 256 rows deep.
-    const long long blocks = static_cast<long long>(row_tiles) * col_tiles;
-    const int want = static_cast<int>(std::max(1LL, cu_count() / blocks));
-    int slices = std::max(1, std::min(want, ceil_div(a.k, 256)));
-    const int span = ceil_div(ceil_div(a.k, slices), kStep) * kStep;
-    slices = ceil_div(a.k, span);
-
     SbParams p{};
     p.m = a.m;
     p.n = a.n;
@@ -766,6 +830,7 @@ bool run_split_bf16(const MatmulArgs& a, const RopeFuse* rope) {
     p.B = static_cast<const int8_t*>(a.B);
     p.scale = a.scale;
     p.direct = slices == 1;
+    p.pair = pair;
     p.accumulate = a.accumulate && p.direct;
     p.out = p.direct ? a.C : scratch(kPartial, static_cast<std::size_t>(slices) * a.m * a.n);
     p.row_tiles = row_tiles;
@@ -804,7 +869,8 @@ bool run_split_bf16(const MatmulArgs& a, const RopeFuse* rope) {
         t.col_base = col_tiles - tail_cols;
         t.xcd_order = 1;
         launch<2>(t, t.row_tiles * tail_cols, raw, a.stream);
-        return fuse;
+        *fused = fuse;
+        return true;
     }
     const int total = static_cast<int>(blocks) * slices;
     switch (RB) {
@@ -813,7 +879,27 @@ bool run_split_bf16(const MatmulArgs& a, const RopeFuse* rope) {
         default: launch<2>(p, total, raw, a.stream); break;
     }
     if (!p.direct) run_reduce_slices(a.m, a.n, slices, p.out, a.scale, a.C, a.accumulate, a.stream);
-    return fuse;
+    *fused = fuse;
+    return true;
+}
+
+}  // namespace
+
+bool run_split_bf16(const MatmulArgs& a, const RopeFuse* rope) {
+    bool fused = false;
+    split_run(a, rope, 0, &fused);
+    return fused;
+}
+
+bool split_bf16_swiglu_supported(const MatmulArgs& a, int hidden) {
+    return hidden > 0 && hidden % 16 == 0 && a.n == 2 * hidden && !a.accumulate &&
+           split_bf16_supports(a) && reinterpret_cast<uintptr_t>(a.C) % 16 == 0;
+}
+
+bool run_split_bf16_swiglu(const MatmulArgs& a, int hidden) {
+    if (!split_bf16_swiglu_supported(a, hidden)) return false;
+    bool fused = false;
+    return split_run(a, nullptr, hidden, &fused);
 }
 
 }  // namespace em

@@ -243,6 +243,53 @@ def test_strip_copy_decode_matches_cpu(tmp_path, monkeypatch, dim, hidden, heads
     unfused.close()
 
 
+@pytest.mark.parametrize("dim,hidden,heads,kv_heads",
+                         [(256, 688, 4, 2), (320, 864, 5, 5), (256, 4608, 4, 2)],
+                         ids=["h688_partial_tile", "h864_mha", "h4608_wide"])
+def test_prefill_swiglu_pair_same_bits(tmp_path, monkeypatch, dim, hidden, heads, kv_heads):
+    # Int8 prefill rows past 16 form silu(gate) * up in the exact-split w13
+    # product's epilogue (each 256-column tile holds 128 gates and their 128
+    # ups); a second model created with EM_MODEL_SWIGLU_FUSION=0 writes the
+    # product and runs swiglu_kernel. Every logit must be the same bits: a
+    # 40-row prefill, a 100-row chunk from position 40, then decode steps
+    # over the caches both wrote; each against the CPU Transformer too.
+    # hidden 688 = 5 x 128 + 48 leaves a last tile of 48 gates; 864 = 6 x 128
+    # + 96; 4608 = 36 x 128.
+    m = e2e_model.fixture_model(heads, kv_heads, False, seed=500 + dim + hidden, dim=dim,
+                                hidden=hidden, vocab=300, seq_len=160)
+    path = str(tmp_path / "model.bin")
+    e2e_model.write_raw(path, m)
+    ck = oracle.RefCheckpoint(lib, path)
+    w = ck.weights()
+    cpu = oracle.RefTransformer(lib, ck, True)
+    monkeypatch.delenv("EM_MODEL_SWIGLU_FUSION", raising=False)
+    paired = em.Model(ck.config, w, q8=True)
+    monkeypatch.setenv("EM_MODEL_SWIGLU_FUSION", "0")
+    unpaired = em.Model(ck.config, w, q8=True)
+    monkeypatch.delenv("EM_MODEL_SWIGLU_FUSION")
+    V = ck.config["vocab_size"]
+    tokens = [(p * 17 + 9) % V for p in range(160)]
+
+    def check(a, b, c, what):
+        assert np.array_equal(a, b), f"{what}: max diff {np.abs(a - b).max()}"
+        tol = 1e-4 * float(np.abs(c).max())
+        assert float(np.abs(a - c).max()) <= tol, what
+        assert int(np.argmax(a)) == int(np.argmax(c)), f"{what}: greedy token"
+
+    print(f"swiglu pair hidden {hidden}: prefill 0..40", flush=True)
+    check(paired.forward(tokens[:40], 0), unpaired.forward(tokens[:40], 0),
+          cpu.run(tokens[:40], 0), "prefill 40")
+    print(f"swiglu pair hidden {hidden}: prefill 40..140", flush=True)
+    check(paired.forward(tokens[40:140], 40), unpaired.forward(tokens[40:140], 40),
+          cpu.run(tokens[40:140], 40), "prefill 40..140")
+    for pos in range(140, 146):
+        print(f"swiglu pair hidden {hidden}: decode {pos}", flush=True)
+        check(paired.forward(tokens[pos], pos), unpaired.forward(tokens[pos], pos),
+              cpu.run([tokens[pos]], pos, True), f"decode at {pos}")
+    paired.close()
+    unpaired.close()
+
+
 @pytest.mark.parametrize("heads,kv_heads", [(4, 4), (4, 2)], ids=["mha", "gqa"])
 def test_prefill_rope_epilogue_same_bits_as_rope_kernel(tmp_path, monkeypatch, heads, kv_heads):
     # Int8 prefill rows send the fused qkv product to the exact-split kernel;
