@@ -211,7 +211,12 @@ __global__ __launch_bounds__(kThreads) void split_a_row_kernel(int m, int k, int
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[st][e] = live && j0 + e < k ? in[j0 + e] : 0.0f;
         }
-        if (w) {
+        if (w && vec4 && j0 + 8 <= k) {
+            const floatx4 g0 = *reinterpret_cast<const floatx4*>(w + j0);
+            const floatx4 g1 = *reinterpret_cast<const floatx4*>(w + j0 + 4);
+            wv[st][0] = g0.x; wv[st][1] = g0.y; wv[st][2] = g0.z; wv[st][3] = g0.w;
+            wv[st][4] = g1.x; wv[st][5] = g1.y; wv[st][6] = g1.z; wv[st][7] = g1.w;
+        } else if (w) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) wv[st][e] = j0 + e < k ? w[j0 + e] : 1.0f;
         }
@@ -800,7 +805,9 @@ bool split_run(const MatmulArgs& a, const RopeFuse* rope, int pair, bool* fused)
         A3 = reinterpret_cast<uint16_t*>(base);
         shifts = reinterpret_cast<int*>(base + plane_floats);
         const int steps = ceil_div(k_pad, 8 * kThreads);
-        const int vec4 = a.k % 4 == 0 && reinterpret_cast<uintptr_t>(a.A) % 16 == 0;
+        // Rows (and the norm weight) read as float4 where 16-byte aligned.
+        const int vec4 = a.k % 4 == 0 && reinterpret_cast<uintptr_t>(a.A) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(a.rms_weight) % 16 == 0;
         auto row = [&](auto kern) {
             hipLaunchKernelGGL(kern, dim3(m_pad), dim3(kThreads), 0, a.stream, a.m, a.k, m_pad,
                                k_pad, vec4, a.A, a.rms_weight, A3, shifts);

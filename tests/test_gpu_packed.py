@@ -433,14 +433,15 @@ def test_python_registration_ends_with_its_tensor():
         pytest.skip("the caching allocator gave another address; the registration ended anyway")
 
 
-@pytest.mark.parametrize("m", [1, 12])
+@pytest.mark.parametrize("m", [1, 12, 64, 200])
 @pytest.mark.parametrize("shape", [(4096, 4096), (288, 864)], ids=lambda s: "x".join(map(str, s)))
 def test_registered_misaligned_norm_weight(shape, m):
     # The norm weight one float past a 16-byte boundary (the reference's
     # MatmulFusion.rms_weight may be any device float pointer,
     # cuda_matmul.h:85-92): the kernels that load it four floats at a time
-    # are passed over for ones that load it per value; within the oracle's
-    # bound, the same bits on a second call.
+    # are passed over for ones that load it per value (the one-row strip
+    # kernel; at 64 and 200 rows the exact split's pre-pass); within the
+    # oracle's bound, the same bits on a second call.
     k, n = shape
     A = inputs.uniform((m, k), -1.0, 1.0, 321)
     q, s = orc.quantize_q8(inputs.normal((k, n), 0.02, 322))
