@@ -294,15 +294,27 @@ struct SbParams {
 // head_size % 4 == 0): two q or k pairs rotated by rope_pair with the
 // tables' row of this position, q back into C, k into the key cache; v
 // into the value cache.
-__device__ __forceinline__ void rope_store(const SbParams& p, int row, int c, floatx4 v) {
+// The angles of columns c .. c + 3 at position pos (q or k columns): the
+// cosines and sines of pairs (cc / 2) % half and the next, which is
+// (cc / 2) % half + 1 (cc % 4 == 0 and half even), loaded as float2s.
+// {cos0, cos1, sin0, sin1}; zeros for value columns.
+__device__ __forceinline__ floatx4 rope_angles(const RopeFuse& r, int pos, int c) {
+    if (c >= r.dim + r.kv_dim) return floatx4{0.f, 0.f, 0.f, 0.f};
+    const int cc = c >= r.dim ? c - r.dim : c, half = r.head_size / 2;
+    const int a0 = pos * half + (cc / 2) % half;
+    const float2 cs = *reinterpret_cast<const float2*>(r.cos_t + a0);
+    const float2 sn = *reinterpret_cast<const float2*>(r.sin_t + a0);
+    return floatx4{cs.x, cs.y, sn.x, sn.y};
+}
+
+__device__ __forceinline__ void rope_put(const SbParams& p, int row, int pos, int c, floatx4 v,
+                                         const floatx4& ang) {
     const RopeFuse& r = p.rope;
-    const int pos = *r.pos + row, half = r.head_size / 2;
     if (c < r.dim + r.kv_dim) {
         const bool is_k = c >= r.dim;
         const int cc = is_k ? c - r.dim : c;
-        const int a0 = pos * half + (cc / 2) % half, a1 = pos * half + (cc / 2 + 1) % half;
-        const float2 y0 = rope_pair(v[0], v[1], r.cos_t[a0], r.sin_t[a0]);
-        const float2 y1 = rope_pair(v[2], v[3], r.cos_t[a1], r.sin_t[a1]);
+        const float2 y0 = rope_pair(v[0], v[1], ang[0], ang[2]);
+        const float2 y1 = rope_pair(v[2], v[3], ang[1], ang[3]);
         float* dst = is_k ? r.kc + static_cast<std::size_t>(pos) * r.kv_dim + cc
                           : p.out + static_cast<std::size_t>(row) * p.n + c;
         *reinterpret_cast<floatx4*>(dst) = floatx4{y0.x, y0.y, y1.x, y1.y};
@@ -310,6 +322,11 @@ __device__ __forceinline__ void rope_store(const SbParams& p, int row, int c, fl
         *reinterpret_cast<floatx4*>(r.vc + static_cast<std::size_t>(pos) * r.kv_dim +
                                     (c - r.dim - r.kv_dim)) = v;
     }
+}
+
+__device__ __forceinline__ void rope_store(const SbParams& p, int row, int c, floatx4 v) {
+    const int pos = *p.rope.pos + row;
+    rope_put(p, row, pos, c, v, rope_angles(p.rope, pos, c));
 }
 
 // One 16-row block of split_bf16_kernel's tile (columns c0 .. c0 + 255,
@@ -578,9 +595,36 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
     // term dropped bits (|a| below 2^-110) or a sum is not finite (an
     // infinite or NaN activation, or an overflow) is not written here but
     // computed again by fma_block once the others are out.
+    //
+    // The epilogue's loads come before its stores: a load placed after a
+    // store that may alias it cannot be moved above it, so each would wait
+    // for its own round trip, one after another. The column scales (the
+    // same columns in every block) and the rows' shifts are loaded before
+    // the blocks; a block's prior C values and RoPE angles before its
+    // stores.
     const int orow = tid / 16, ocol = (tid % 16) * 16;
     __shared__ int any_bad[4];
     uint32_t redo = 0;  // RAW: bit rb set for each block fma_block recomputes
+    // PAIR: gates pp .. pp + 7 of the tile (and their ups) per thread.
+    const int pp = (tid % 16) * 8;
+    floatx4 esc[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        esc[q] = floatx4{1.f, 1.f, 1.f, 1.f};
+        if constexpr (PAIR) {
+            // q = 0, 1: the gates' scales; 2, 3: the ups'.
+            const int c = min(c0 + pp + 4 * (q & 1), p.pair - 4);
+            esc[q] = *reinterpret_cast<const floatx4*>(p.scale + (q < 2 ? c : p.pair + c));
+        } else if (p.direct) {
+            const int c = min(c0 + ocol + 4 * q, p.n - 4);
+            esc[q] = *reinterpret_cast<const floatx4*>(p.scale + c);
+        }
+    }
+    int esh[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+        esh[rb] = RAW ? 0 : -p.shifts[m0 + 16 * rb + (PAIR ? tid / 16 : orow)];  // < m_pad
+    const int rpos0 = p.direct && p.rope.pos ? *p.rope.pos : 0;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
         if (rb > 0) __syncthreads();
@@ -597,7 +641,7 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
             // Eight gates of one row per thread and their ups 128 columns
             // on, each summed over the waves in order as below, scaled as C
             // would be written, then paired.
-            const int prow = tid / 16, pp = (tid % 16) * 8;
+            const int prow = tid / 16;
             const int prow_m = m0 + 16 * rb + prow;
             floatx4 gv[2], uv[2];
 #pragma unroll
@@ -612,13 +656,13 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
                 }
             }
             if (prow_m < p.m) {
-                const int sh = -p.shifts[prow_m];
+                const int sh = esh[rb];
 #pragma unroll
                 for (int q = 0; q < 2; ++q) {
                     const int c = c0 + pp + 4 * q;
                     if (c >= p.pair) break;
-                    floatx4 gx = gv[q] * *reinterpret_cast<const floatx4*>(p.scale + c);
-                    floatx4 ux = uv[q] * *reinterpret_cast<const floatx4*>(p.scale + p.pair + c);
+                    const floatx4 gx = gv[q] * esc[q];
+                    const floatx4 ux = uv[q] * esc[2 + q];
                     floatx4 y;
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
@@ -659,24 +703,38 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
             // Pre-split planes: the row's scale undone, after the column
             // scale into C, before it into the partials (reduce_slices
             // applies it).
-            const int sh = RAW ? 0 : -p.shifts[row];
+            const int sh = esh[rb];
+            const bool rope = p.direct && p.rope.pos;
+            const int rpos = rpos0 + row;
+            // This block's loads: prior C (accumulating) or RoPE angles.
+            floatx4 extra[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int c = c0 + ocol + 4 * q;
+                extra[q] = floatx4{0.f, 0.f, 0.f, 0.f};
+                if (c >= p.n) continue;
+                if (rope)
+                    extra[q] = rope_angles(p.rope, rpos, c);
+                else if (p.direct && p.accumulate)
+                    extra[q] = *reinterpret_cast<const floatx4*>(p.out + static_cast<std::size_t>(row) * p.n + c);
+            }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int c = c0 + ocol + 4 * q;
                 if (c >= p.n) break;
                 floatx4 x = v[q];
-                if (p.direct) x *= *reinterpret_cast<const floatx4*>(p.scale + c);
+                if (p.direct) x *= esc[q];
                 if constexpr (!RAW) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) x[e] = __builtin_ldexpf(x[e], sh);
                 }
                 if (p.direct) {
-                    if (p.rope.pos) {
-                        rope_store(p, row, c, x);
+                    if (rope) {
+                        rope_put(p, row, rpos, c, x, extra[q]);
                         continue;
                     }
                     floatx4* o = reinterpret_cast<floatx4*>(p.out + static_cast<std::size_t>(row) * p.n + c);
-                    *o = p.accumulate ? *o + x : x;
+                    *o = p.accumulate ? extra[q] + x : x;
                 } else {
                     *reinterpret_cast<floatx4*>(
                         p.out + (static_cast<std::size_t>(place.slice) * p.m + row) * p.n + c) = x;
