@@ -24,11 +24,11 @@
 // Slices. k is cut into slices so the grid covers the CUs (4096^2: 64
 // tiles x 4 slices). Within a workgroup the four waves take interleaved
 // 32-row chunks and are added through LDS in wave order. Each workgroup
-// then stores its slice's sums as agent-scope atomic stores (device-
-// coherent, no cache write-back), waits for them, and counts itself in at
-// its tile's counter (one relaxed agent-scope atomic add). The workgroup
-// that counts in last adds the tile's slices in slice order (its own from
-// LDS, the others by agent-scope atomic loads), applies the scale, norm and
+// then stores its slice's sums as device-coherent (sc1) buffer stores (no
+// cache write-back), waits for them, and counts itself in at its tile's
+// counter (one relaxed agent-scope atomic add). The workgroup that counts
+// in last adds the tile's slices in slice order (its own from registers,
+// the others by sc1 buffer loads), applies the scale, norm and
 // accumulation, stores C and sets the counter back to zero for the next
 // call. The sum order is fixed, so repeated calls give the same bits,
 // whichever workgroup arrives last. Counters are library memory, zero when
@@ -300,6 +300,35 @@ __global__ __launch_bounds__(kNT) void strip_split_kernel(SsParams p) {
         }
     }
 
+    // Item i of this thread: row it / 16 of the tile, columns 4 (it % 16) ..
+    // 4 (it % 16) + 3, for it = tid + kNT i below 16 MR.
+    auto item = [&](int i, int& row, int& q) {
+        const int it = tid + kNT * i;
+        row = it >> 4;
+        q = it & 15;
+        return it < MR * 16;
+    };
+    // The epilogue's column scales, issued here so that their latency passes
+    // behind the wave sums' staging and the slice exchange, not after the
+    // last workgroup's sums (n is a multiple of 16, so c < n covers c + 3).
+    // Without k slices the prior C (accumulate) comes with them; with slices
+    // only the last workgroup of the tile loads it, beside the others' sums.
+    floatx4 esc[NI], eprior[NI];
+    auto load_prior = [&](int i, int row, int c) {
+        if (p.accumulate)
+            eprior[i] = *reinterpret_cast<const floatx4*>(p.C + static_cast<std::size_t>(row) * p.n + c);
+    };
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        int row, q;
+        esc[i] = eprior[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+        if (!item(i, row, q)) continue;
+        const int c = tile * kCols + 4 * q;
+        if (row >= p.m || c >= p.n) continue;
+        esc[i] = *reinterpret_cast<const floatx4*>(p.scale + c);
+        if constexpr (SB == 1) load_prior(i, row, c);
+    }
+
     // Wave sums into LDS: lane (g, j) holds rows 4g + r, columns 4j .. 4j + 3.
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
@@ -321,14 +350,6 @@ __global__ __launch_bounds__(kNT) void strip_split_kernel(SsParams p) {
     }
     __syncthreads();
 
-    // Item i of this thread: row it / 16 of the tile, columns 4 (it % 16) ..
-    // 4 (it % 16) + 3, for it = tid + kNT i below 16 MR.
-    auto item = [&](int i, int& row, int& q) {
-        const int it = tid + kNT * i;
-        row = it >> 4;
-        q = it & 15;
-        return it < MR * 16;
-    };
     floatx4 v[NI];
     float sq[NI];
 #pragma unroll
@@ -403,6 +424,13 @@ __global__ __launch_bounds__(kNT) void strip_split_kernel(SsParams p) {
         // past the slice count read offset 0, one shared line), then added
         // in slice order with this slice's own from registers.
         const uint32_t tile0 = static_cast<uint32_t>(tile * p.slices * MR);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            int row, q;
+            if (!item(i, row, q)) continue;
+            const int c = tile * kCols + 4 * q;
+            if (row < p.m && c < p.n) load_prior(i, row, c);
+        }
         floatx4 xs[NI][SB];
         float ys[NI][SB];
 #pragma unroll
@@ -447,9 +475,9 @@ __global__ __launch_bounds__(kNT) void strip_split_kernel(SsParams p) {
         if (row >= p.m || c >= p.n) continue;
         floatx4 x = v[i];
         if constexpr (NORM) x *= 1.0f / sqrtf(sq[i] / static_cast<float>(p.k) + kRmsEps);
-        x *= *reinterpret_cast<const floatx4*>(p.scale + c);
+        x *= esc[i];
         floatx4* o = reinterpret_cast<floatx4*>(p.C + static_cast<std::size_t>(row) * p.n + c);
-        *o = p.accumulate ? *o + x : x;
+        *o = p.accumulate ? eprior[i] + x : x;
     }
 }
 
