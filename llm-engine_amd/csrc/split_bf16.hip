@@ -468,6 +468,34 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
     const int kb = place.slice * p.k_span;
     const int ke = min(p.k, kb + p.k_span);
 
+    // The epilogue's column scales (the same columns in every row block)
+    // and row shifts, loaded before the first chunk: issued after the
+    // chunks, their wait would also wait for the ring's re-reads past the
+    // last chunk, and their registers could only be written once those
+    // re-reads had landed. Thread (orow, ocol) ends up with row orow,
+    // columns ocol .. ocol + 15 of each block; PAIR: gates pp .. pp + 7 of
+    // the tile (and their ups).
+    const int orow = tid / 16, ocol = (tid % 16) * 16;
+    const int pp = (tid % 16) * 8;
+    floatx4 esc[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        esc[q] = floatx4{1.f, 1.f, 1.f, 1.f};
+        if constexpr (PAIR) {
+            // q = 0, 1: the gates' scales; 2, 3: the ups'.
+            const int c = min(c0 + pp + 4 * (q & 1), p.pair - 4);
+            esc[q] = *reinterpret_cast<const floatx4*>(p.scale + (q < 2 ? c : p.pair + c));
+        } else if (p.direct) {
+            const int c = min(c0 + ocol + 4 * q, p.n - 4);
+            esc[q] = *reinterpret_cast<const floatx4*>(p.scale + c);
+        }
+    }
+    int esh[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+        esh[rb] = RAW ? 0 : -p.shifts[m0 + 16 * rb + (PAIR ? tid / 16 : orow)];  // < m_pad
+    const int rpos0 = p.direct && p.rope.pos ? *p.rope.pos : 0;
+
     floatx4 acc[RB][16];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
@@ -598,33 +626,12 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
     //
     // The epilogue's loads come before its stores: a load placed after a
     // store that may alias it cannot be moved above it, so each would wait
-    // for its own round trip, one after another. The column scales (the
-    // same columns in every block) and the rows' shifts are loaded before
-    // the blocks; a block's prior C values and RoPE angles before its
-    // stores.
-    const int orow = tid / 16, ocol = (tid % 16) * 16;
+    // for its own round trip, one after another (a wait for a load is also
+    // a wait for every earlier store on this target). The column scales and
+    // the rows' shifts were loaded before the chunks; a block's prior C
+    // values and RoPE angles are loaded before its stores.
     __shared__ int any_bad[4];
     uint32_t redo = 0;  // RAW: bit rb set for each block fma_block recomputes
-    // PAIR: gates pp .. pp + 7 of the tile (and their ups) per thread.
-    const int pp = (tid % 16) * 8;
-    floatx4 esc[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        esc[q] = floatx4{1.f, 1.f, 1.f, 1.f};
-        if constexpr (PAIR) {
-            // q = 0, 1: the gates' scales; 2, 3: the ups'.
-            const int c = min(c0 + pp + 4 * (q & 1), p.pair - 4);
-            esc[q] = *reinterpret_cast<const floatx4*>(p.scale + (q < 2 ? c : p.pair + c));
-        } else if (p.direct) {
-            const int c = min(c0 + ocol + 4 * q, p.n - 4);
-            esc[q] = *reinterpret_cast<const floatx4*>(p.scale + c);
-        }
-    }
-    int esh[RB];
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
-        esh[rb] = RAW ? 0 : -p.shifts[m0 + 16 * rb + (PAIR ? tid / 16 : orow)];  // < m_pad
-    const int rpos0 = p.direct && p.rope.pos ? *p.rope.pos : 0;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
         if (rb > 0) __syncthreads();
@@ -704,7 +711,27 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
             // scale into C, before it into the partials (reduce_slices
             // applies it).
             const int sh = esh[rb];
-            const bool rope = p.direct && p.rope.pos;
+            auto unshift = [&](floatx4 x) {
+                if constexpr (!RAW) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) x[e] = __builtin_ldexpf(x[e], sh);
+                }
+                return x;
+            };
+            if (!p.direct) {
+                // A k slice's sums into the partials. This path loads
+                // nothing: a load here, even one on the other path only,
+                // would make each store wait for the ones before it.
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int c = c0 + ocol + 4 * q;
+                    if (c >= p.n) break;
+                    *reinterpret_cast<floatx4*>(
+                        p.out + (static_cast<std::size_t>(place.slice) * p.m + row) * p.n + c) = unshift(v[q]);
+                }
+                continue;
+            }
+            const bool rope = p.rope.pos != nullptr;  // direct products only
             const int rpos = rpos0 + row;
             // This block's loads: prior C (accumulating) or RoPE angles.
             floatx4 extra[4];
@@ -715,30 +742,20 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
                 if (c >= p.n) continue;
                 if (rope)
                     extra[q] = rope_angles(p.rope, rpos, c);
-                else if (p.direct && p.accumulate)
+                else if (p.accumulate)
                     extra[q] = *reinterpret_cast<const floatx4*>(p.out + static_cast<std::size_t>(row) * p.n + c);
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int c = c0 + ocol + 4 * q;
                 if (c >= p.n) break;
-                floatx4 x = v[q];
-                if (p.direct) x *= esc[q];
-                if constexpr (!RAW) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) x[e] = __builtin_ldexpf(x[e], sh);
+                const floatx4 x = unshift(v[q] * esc[q]);
+                if (rope) {
+                    rope_put(p, row, rpos, c, x, extra[q]);
+                    continue;
                 }
-                if (p.direct) {
-                    if (rope) {
-                        rope_put(p, row, rpos, c, x, extra[q]);
-                        continue;
-                    }
-                    floatx4* o = reinterpret_cast<floatx4*>(p.out + static_cast<std::size_t>(row) * p.n + c);
-                    *o = p.accumulate ? extra[q] + x : x;
-                } else {
-                    *reinterpret_cast<floatx4*>(
-                        p.out + (static_cast<std::size_t>(place.slice) * p.m + row) * p.n + c) = x;
-                }
+                floatx4* o = reinterpret_cast<floatx4*>(p.out + static_cast<std::size_t>(row) * p.n + c);
+                *o = p.accumulate ? extra[q] + x : x;
             }
         }
     }
