@@ -307,6 +307,20 @@ __device__ __forceinline__ floatx4 rope_angles(const RopeFuse& r, int pos, int c
     return floatx4{cs.x, cs.y, sn.x, sn.y};
 }
 
+// The same without a branch: value columns load the angles of their offset
+// in the value part (any valid pair; rope_put does not read them), so the
+// loads are unconditional and no merge of loaded and constant values makes
+// a later instruction wait for them.
+__device__ __forceinline__ floatx4 rope_angles_any(const RopeFuse& r, int pos, int c) {
+    const int kv_end = r.dim + r.kv_dim;
+    const int cc = c >= kv_end ? c - kv_end : c >= r.dim ? c - r.dim : c;
+    const int half = r.head_size / 2;
+    const int a0 = pos * half + (cc / 2) % half;
+    const float2 cs = *reinterpret_cast<const float2*>(r.cos_t + a0);
+    const float2 sn = *reinterpret_cast<const float2*>(r.sin_t + a0);
+    return floatx4{cs.x, cs.y, sn.x, sn.y};
+}
+
 __device__ __forceinline__ void rope_put(const SbParams& p, int row, int pos, int c, floatx4 v,
                                          const floatx4& ang) {
     const RopeFuse& r = p.rope;
@@ -452,9 +466,14 @@ __device__ __forceinline__ bf16x8 column(const uint4 (&b)[8], int t) {
 // column t < 128 is gate c0 + t and column 128 + t its up; the epilogue
 // writes silu(g) * u of the finished, scaled values: the bits of the
 // product written to C followed by the forward pass's SwiGLU kernel.
-template <int RB, bool RAW, bool WHOLE, bool PAIR = false>
+// EPI, the direct product's epilogue: kStore (C = the sums, or partials
+// when k is split), kAccumulate (C += the sums), kRope (the qkv epilogue).
+constexpr int kStore = 0, kAccumulate = 1, kRope = 2;
+
+template <int RB, bool RAW, bool WHOLE, bool PAIR = false, int EPI = kStore>
 __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
     static_assert(!(PAIR && RAW), "the SwiGLU pair reads pre-split planes");
+    static_assert(!(PAIR && EPI != kStore), "the SwiGLU pair writes its own output");
     __shared__ __attribute__((aligned(16))) floatx4 tile[4 * 16 * kTile / 4];
 
     const int tid = threadIdx.x;
@@ -485,7 +504,8 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
             // q = 0, 1: the gates' scales; 2, 3: the ups'.
             const int c = min(c0 + pp + 4 * (q & 1), p.pair - 4);
             esc[q] = *reinterpret_cast<const floatx4*>(p.scale + (q < 2 ? c : p.pair + c));
-        } else if (p.direct) {
+        } else {
+            // Unused when k is split (reduce_slices scales the sums).
             const int c = min(c0 + ocol + 4 * q, p.n - 4);
             esc[q] = *reinterpret_cast<const floatx4*>(p.scale + c);
         }
@@ -494,7 +514,7 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
         esh[rb] = RAW ? 0 : -p.shifts[m0 + 16 * rb + (PAIR ? tid / 16 : orow)];  // < m_pad
-    const int rpos0 = p.direct && p.rope.pos ? *p.rope.pos : 0;
+    const int rpos0 = EPI == kRope ? *p.rope.pos : 0;
 
     floatx4 acc[RB][16];
 #pragma unroll
@@ -625,13 +645,31 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
     // computed again by fma_block once the others are out.
     //
     // The epilogue's loads come before its stores: a load placed after a
-    // store that may alias it cannot be moved above it, so each would wait
-    // for its own round trip, one after another (a wait for a load is also
-    // a wait for every earlier store on this target). The column scales and
-    // the rows' shifts were loaded before the chunks; a block's prior C
-    // values and RoPE angles are loaded before its stores.
+    // store that may alias it cannot be moved above it, and a wait for a
+    // load is also a wait for every store issued before it on this target,
+    // so loads between stores would make each store wait for the last. The
+    // column scales and the rows' shifts were loaded before the chunks;
+    // every block's prior C values (kAccumulate) or RoPE angles (kRope) are
+    // loaded here, before any store, unconditionally (rows and columns
+    // clamped into range, their values then unused), so that no merge of a
+    // loaded and a constant value makes a later instruction wait.
     __shared__ int any_bad[4];
     uint32_t redo = 0;  // RAW: bit rb set for each block fma_block recomputes
+    floatx4 extra[EPI == kStore ? 1 : RB][4];
+    if constexpr (EPI != kStore) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int row = min(m0 + 16 * rb + orow, p.m - 1);
+                const int c = min(c0 + ocol + 4 * q, p.n - 4);
+                if constexpr (EPI == kRope)
+                    extra[rb][q] = rope_angles_any(p.rope, rpos0 + row, c);
+                else
+                    extra[rb][q] = *reinterpret_cast<const floatx4*>(
+                        p.out + static_cast<std::size_t>(row) * p.n + c);
+            }
+    }
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
         if (rb > 0) __syncthreads();
@@ -718,10 +756,8 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
                 }
                 return x;
             };
-            if (!p.direct) {
-                // A k slice's sums into the partials. This path loads
-                // nothing: a load here, even one on the other path only,
-                // would make each store wait for the ones before it.
+            if (EPI == kStore && !p.direct) {
+                // A k slice's sums into the partials.
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int c = c0 + ocol + 4 * q;
@@ -731,31 +767,20 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
                 }
                 continue;
             }
-            const bool rope = p.rope.pos != nullptr;  // direct products only
-            const int rpos = rpos0 + row;
-            // This block's loads: prior C (accumulating) or RoPE angles.
-            floatx4 extra[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int c = c0 + ocol + 4 * q;
-                extra[q] = floatx4{0.f, 0.f, 0.f, 0.f};
-                if (c >= p.n) continue;
-                if (rope)
-                    extra[q] = rope_angles(p.rope, rpos, c);
-                else if (p.accumulate)
-                    extra[q] = *reinterpret_cast<const floatx4*>(p.out + static_cast<std::size_t>(row) * p.n + c);
-            }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int c = c0 + ocol + 4 * q;
                 if (c >= p.n) break;
                 const floatx4 x = unshift(v[q] * esc[q]);
-                if (rope) {
-                    rope_put(p, row, rpos, c, x, extra[q]);
-                    continue;
+                if constexpr (EPI == kRope) {
+                    rope_put(p, row, rpos0 + row, c, x, extra[rb][q]);
+                } else {
+                    floatx4* o = reinterpret_cast<floatx4*>(p.out + static_cast<std::size_t>(row) * p.n + c);
+                    if constexpr (EPI == kAccumulate)
+                        *o = extra[rb][q] + x;
+                    else
+                        *o = x;
                 }
-                floatx4* o = reinterpret_cast<floatx4*>(p.out + static_cast<std::size_t>(row) * p.n + c);
-                *o = p.accumulate ? extra[q] + x : x;
             }
         }
     }
@@ -768,6 +793,24 @@ __global__ __launch_bounds__(kThreads) void split_bf16_kernel(SbParams p) {
     }
 }
 
+template <int RB, int EPI>
+void launch_epi(const SbParams& p, int blocks, bool raw, bool whole, hipStream_t s) {
+    const dim3 grid(blocks), block(kThreads);
+    if constexpr (EPI != kRope) {  // the RoPE epilogue only follows a pre-pass
+        if (raw) {
+            if (whole)
+                hipLaunchKernelGGL((split_bf16_kernel<RB, true, true, false, EPI>), grid, block, 0, s, p);
+            else
+                hipLaunchKernelGGL((split_bf16_kernel<RB, true, false, false, EPI>), grid, block, 0, s, p);
+            return;
+        }
+    }
+    if (whole)
+        hipLaunchKernelGGL((split_bf16_kernel<RB, false, true, false, EPI>), grid, block, 0, s, p);
+    else
+        hipLaunchKernelGGL((split_bf16_kernel<RB, false, false, false, EPI>), grid, block, 0, s, p);
+}
+
 template <int RB>
 void launch(const SbParams& p, int blocks, bool raw, hipStream_t s) {
     const bool whole = p.k % kChunk == 0;
@@ -778,15 +821,11 @@ void launch(const SbParams& p, int blocks, bool raw, hipStream_t s) {
             hipLaunchKernelGGL((split_bf16_kernel<RB, false, false, true>), dim3(blocks), dim3(kThreads), 0, s, p);
         return;
     }
-    if (raw && whole) {
-        hipLaunchKernelGGL((split_bf16_kernel<RB, true, true>), dim3(blocks), dim3(kThreads), 0, s, p);
-    } else if (raw) {
-        hipLaunchKernelGGL((split_bf16_kernel<RB, true, false>), dim3(blocks), dim3(kThreads), 0, s, p);
-    } else if (whole) {
-        hipLaunchKernelGGL((split_bf16_kernel<RB, false, true>), dim3(blocks), dim3(kThreads), 0, s, p);
-    } else {
-        hipLaunchKernelGGL((split_bf16_kernel<RB, false, false>), dim3(blocks), dim3(kThreads), 0, s, p);
-    }
+    if (p.rope.pos)  // direct, pre-split (split_run fuses RoPE only then)
+        return launch_epi<RB, kRope>(p, blocks, raw, whole, s);
+    if (p.accumulate)  // direct (the partials of a k split are added by reduce_slices)
+        return launch_epi<RB, kAccumulate>(p, blocks, raw, whole, s);
+    launch_epi<RB, kStore>(p, blocks, raw, whole, s);
 }
 
 }  // namespace
@@ -924,7 +963,7 @@ bool split_run(const MatmulArgs& a, const RopeFuse* rope, int pair, bool* fused)
     // XCD-grouped order, which gives each XCD a contiguous run of B (4096 x
     // 32000, m = 5: 26.6 against 28.6 us in plain order).
     p.xcd_order = row_tiles == 1 && col_tiles % 8 == 0 ? 0 : 1;
-    const bool fuse = rope && p.direct && !a.accumulate && rope->head_size % 4 == 0 &&
+    const bool fuse = rope && p.direct && !raw && !a.accumulate && rope->head_size % 4 == 0 &&
                       rope->dim % 4 == 0 && rope->kv_dim % 4 == 0 &&
                       a.n == rope->dim + 2 * rope->kv_dim;
     if (fuse) p.rope = *rope;
