@@ -302,7 +302,7 @@ def llama7b_model_case(em, torch, n_layers: int = 2, n_kv_heads: int = 32, seq_l
 
 
 def stories15m_case(em, torch, steps: int = 98):
-    """BASELINE config 4's shape through the device-resident forward pass:
+    """The stories15M end-to-end case through the device-resident forward pass:
     stories15M (dim 288, 6 layers, 6 heads, hidden 768, vocab 32000, seq 256),
     random weights ~N(0, 0.02), a 158-token prefill then `steps` greedy
     decodes; host-timed em_model_forward calls (logits downloaded per call)."""
@@ -891,7 +891,7 @@ def floor_study(em, torch, reps: int = 20) -> dict:
 
 
 def floor_study_fp32(em, torch, reps: int = 20) -> dict:
-    """What bounds one fp32 m = 1 4096^2 call (BASELINE configs[0]'s shape on
+    """What bounds one fp32 m = 1 4096^2 call (the fp32 decode configuration on
     the GPU), with the bench's method (HIP-graph replay of back-to-back
     dependent launches over 10 rotating 64 MiB copies, 640 MiB):
       empty     an empty 256-workgroup launch

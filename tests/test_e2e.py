@@ -1,4 +1,4 @@
-"""the stories15M-shaped Llama forward with every matmul
+"""The stories15M-shaped Llama forward (the benchmark's end-to-end case) with every matmul
 on this build's kernels gives the same greedy token stream as the CPU path.
 
 Both sides run the reference's own model code (model.cpp, ops.cpp,

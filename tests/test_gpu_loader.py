@@ -69,7 +69,7 @@ def test_load_matches_reference_loader(tmp_path, heads, kv_heads, shared, wtype)
 
 @pytest.mark.parametrize("shared", [True, False], ids=["tied", "untied"])
 def test_stories15m_shape(tmp_path, shared):
-    # BASELINE config 4's shape (dim 288, 6 layers, hidden 768, vocab 32000):
+    # The stories15M shape (dim 288, 6 layers, hidden 768, vocab 32000):
     # the 32000 x 288 sections span several 64 MiB staging chunks' worth of
     # rows only for the classifier; arrays and logits as above.
     c = e2e_model.STORIES15M

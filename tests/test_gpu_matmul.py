@@ -321,7 +321,7 @@ def test_graph_replay_matches_eager():
         del extra
 
 
-# ---- BASELINE config shapes at full size -----------------------------------
+# ---- The benchmark configurations' shapes at full size --------------------
 
 @pytest.mark.parametrize("m", [1, 4, 16, 64])
 def test_config2_int8_gemv_4096(m):

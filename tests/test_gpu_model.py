@@ -7,7 +7,7 @@ and int8 weights; decode over the whole context, prefill in chunks of 1, 1
 and 5 rows, a decode step on that cache and a whole-context prefill that
 rewinds over it (:57-79), every logit within the reference's 1e-4 (:31); and
 the same rejections as the CPU model, after which the cache still works
-(:91-106). Then BASELINE config 4 at the stories15M shape through this
+(:91-106). Then the stories15M end-to-end case through this
 build's own forward pass: 158-token prefill and 98 greedy decodes, token
 stream identical to the CPU Transformer's.
 """
