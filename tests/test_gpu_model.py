@@ -290,16 +290,18 @@ def test_prefill_swiglu_pair_same_bits(tmp_path, monkeypatch, dim, hidden, heads
     unpaired.close()
 
 
+@pytest.mark.parametrize("dim", [256, 240])
 @pytest.mark.parametrize("heads,kv_heads", [(4, 4), (4, 2)], ids=["mha", "gqa"])
-def test_prefill_rope_epilogue_same_bits_as_rope_kernel(tmp_path, monkeypatch, heads, kv_heads):
+def test_prefill_rope_epilogue_same_bits_as_rope_kernel(tmp_path, monkeypatch, heads, kv_heads, dim):
     # Int8 prefill rows send the fused qkv product to the exact-split kernel;
-    # with no k split (k = dim = 256 here) it rotates q and k and writes the
-    # caches in its epilogue. A second model created with
+    # with no k split (k = dim here) it rotates q and k and writes the
+    # caches in its epilogue (dim 240: k not a whole number of 32-row chunks,
+    # head size 60). A second model created with
     # EM_PREFILL_ROPE_FUSION=0 writes qkv and runs rope_cache_kernel
     # instead. Every logit must be the same bits: prefill from 0, a second
     # prefill chunk from position 40 (angles taken at pos + row) and decode
     # steps that read the caches both wrote. Against the CPU Transformer too.
-    m = e2e_model.fixture_model(heads, kv_heads, False, seed=300 + heads + kv_heads, dim=256,
+    m = e2e_model.fixture_model(heads, kv_heads, False, seed=300 + heads + kv_heads, dim=dim,
                                 hidden=688, vocab=300, seq_len=128)
     path = str(tmp_path / "model.bin")
     e2e_model.write_raw(path, m)
